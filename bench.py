@@ -1,0 +1,165 @@
+#!/usr/bin/env python3
+"""MoE-FFN throughput on one MI355X: tokens/s of the top-k MoE feed-forward block.
+
+Default workload: dim 3072, 8 experts, top-2, SwiGLU hidden 8192, bf16, 14,232
+rows (three guidance branches of the 8B preset stacked: 3 x (4680 video + 64
+text)).  Inputs are synthetic and seeded (nomas_moe.workloads); weights are
+random-init of that architecture.  One step = one full forward (router,
+scan, dispatch, gate/up GEMM, down GEMM, combine) with x already resident in
+HBM.  Prints one JSON line.
+
+  python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "hy-nomas-rs_amd"))
+
+METRIC = "MoE-FFN tokens/s at dim3072 E8 top2 bf16; % of bf16 MFMA and HBM peak"
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA
+PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
+
+
+def algorithmic(w, b):
+    """Algorithmic flops / bytes per launch of each stage (fixed definitions)."""
+    T, D, E, k, H = w.rows, w.dim, w.experts, w.top_k, w.hidden
+    A = T * k
+    return {
+        "gemm_gate_up_flops": 4.0 * A * D * H,
+        "gemm_down_flops": 2.0 * A * D * H,
+        "router_bytes": T * D * b + E * D * b + 8 * T * k,
+        "dispatch_bytes": T * D * b + A * D * b + 8 * A,
+        "combine_bytes": A * D * b + 8 * A + T * D * b,
+    }
+
+
+def cpu_baseline(w, params, x, target_s=12.0):
+    """The reference algorithm (every expert on every row, f32) on host cores,
+    timed on a bounded prefix of the workload's rows."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle as O
+    from nomas_moe import workloads as wl
+
+    p, _ = wl.oracle_params(params, w.experts)
+    probe = 4
+    t0 = time.perf_counter()
+    O.forward_dense_f32(x[:probe], p, w.top_k)
+    dt = time.perf_counter() - t0
+    rows = int(max(probe, min(w.rows, 1024, probe * target_s / max(dt, 1e-3))))
+    t0 = time.perf_counter()
+    O.forward_dense_f32(x[:rows], p, w.top_k)
+    dt = time.perf_counter() - t0
+    return {
+        "value": rows / dt,
+        "unit": "tokens/s",
+        "cores": O.num_threads(),
+        "kind": "port",
+        "sample": f"first {rows} of {w.rows} rows, faithful dense f32 (all {w.experts} experts "
+                  f"per row, as the reference evaluates), {dt:.1f} s",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="cfg8b")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: the MoE "
+              "feed-forward path here is single-GPU (no collectives).", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+    import nomas_moe as nm
+    from nomas_moe import workloads as wl
+
+    w = wl.WORKLOADS[args.workload]
+    dt = nm.DataType.of(w.dtype)
+    print(f"[bench] workload {w.name}: rows={w.rows} D={w.dim} E={w.experts} k={w.top_k} "
+          f"H={w.hidden} {w.dtype}", file=sys.stderr, flush=True)
+    params = wl.make_params(w)
+    x = wl.make_x(w)
+    cfg = nm.MoeConfig(w.experts, w.top_k, 0.0, 0)
+    layer = nm.MoeLayer.from_source(nm.Weights.from_tensors(params, dt), wl.moe_path(), w.dim,
+                                    w.hidden, cfg)
+    raw = nm.to_model_dtype(x, dt)
+    xd = torch.from_numpy(raw.view(np.int16) if raw.dtype == np.uint16 else raw)
+    xd = xd.view(dt.torch).cuda()
+    y = torch.empty_like(xd)
+    stream = torch.cuda.current_stream()
+    for _ in range(args.warmup):
+        layer.forward(xd, out=y)
+    torch.cuda.synchronize()
+    layer.set_profiling(True)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(args.steps):
+        layer.forward(xd, out=y)
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    stages = layer.stage_times()
+    layer.set_profiling(False)
+    finite = bool(torch.isfinite(y.float()).all())
+    print(f"[bench] {ms:.3f} ms/step, stages {stages}, finite={finite}", file=sys.stderr, flush=True)
+
+    b = 2 if w.dtype != "f32" else 4
+    alg = algorithmic(w, b)
+    gu_tf = alg["gemm_gate_up_flops"] / (stages["gemm_gate_up"] * 1e-3) / 1e12
+    dn_tf = alg["gemm_down_flops"] / (stages["gemm_down"] * 1e-3) / 1e12
+    both_tf = (alg["gemm_gate_up_flops"] + alg["gemm_down_flops"]) / (
+        (stages["gemm_gate_up"] + stages["gemm_down"]) * 1e-3) / 1e12
+    gbps = {s: alg[s + "_bytes"] / (stages[s] * 1e-3) / 1e9
+            for s in ("router", "dispatch", "combine")}
+    result = {
+        "metric": METRIC,
+        "value": w.rows / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": w.dtype,
+        "data": "synthetic (seeded N(0,1) rows, random-init weights of this shape)",
+        "config": {"workload": f"{w.name}: {w.note}", "rows": w.rows, "dim": w.dim,
+                   "experts": w.experts, "top_k": w.top_k, "hidden": w.hidden},
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "gemm_gate_up (grouped gate/up GEMM + SwiGLU)",
+            "achieved": gu_tf,
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": gu_tf / PEAK_BF16_TFLOPS,
+            "traffic": None,
+        },
+        "stages_ms": stages,
+        "gemm_tflops": {"gate_up": gu_tf, "down": dn_tf, "both": both_tf,
+                        "both_frac": both_tf / PEAK_BF16_TFLOPS},
+        "hbm_gbps": gbps,
+        "hbm_frac": {s: v / PEAK_HBM_GBPS for s, v in gbps.items()},
+        "output_finite": finite,
+    }
+    if not args.no_cpu_baseline:
+        wparams = {k: nm.widen(nm.to_model_dtype(v, dt), dt) for k, v in params.items()}
+        result["cpu_baseline"] = cpu_baseline(w, wparams, nm.widen(raw, dt))
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

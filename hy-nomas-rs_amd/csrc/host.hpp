@@ -1,0 +1,141 @@
+// Host-side C++ of the MoE feed-forward block: the layer object behind the C
+// ABI, the weight sources (random init, safetensors, host arrays) and the
+// error convention.
+#pragma once
+
+#include <cstdint>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/nomas_moe.h"
+#include "kernels.hpp"
+
+namespace nomas {
+
+// ---- errors ---------------------------------------------------------------
+// Thread-local last error; functions return a nomas_status code.
+int set_error(int code, const char* fmt, ...);
+const char* last_error();
+void clear_error();
+
+// ---- generator (generator.cpp) -------------------------------------------
+uint64_t path_seed(uint64_t seed, const char* path);
+void randn_affine(uint64_t seed, double mean, double std, int64_t n, float* out);
+uint16_t f32_to_bf16_bits(float f);
+float bf16_bits_to_f32(uint16_t b);
+uint16_t f32_to_f16_bits(float f);
+float f16_bits_to_f32(uint16_t b);
+
+// ---- safetensors (safetensors.cpp) ---------------------------------------
+struct StTensor {
+    std::string dtype;           // "F32", "F64", "BF16", "F16", ...
+    std::vector<int64_t> shape;
+    std::vector<uint8_t> data;   // raw little-endian payload
+};
+
+// Reads the named tensors of `files` (later files override earlier ones).
+// Tensors not present are left out of `out`.  Returns a nomas_status.
+int read_safetensors(const std::vector<std::string>& files, const std::vector<std::string>& names,
+                     std::map<std::string, StTensor>* out);
+
+// Converts a safetensors payload to f32 (F32/F64/BF16/F16 sources).
+int st_to_f32(const StTensor& t, std::vector<float>* out);
+
+// ---- the layer -----------------------------------------------------------
+
+// Parameters of one Lin in f32, reference (out, in) layout.
+struct LinF32 {
+    std::vector<float> w;
+    std::vector<float> b;  // empty = no bias / zero bias
+};
+
+// Expert and router parameters in f32 before rounding to the model dtype.
+struct MoeParamsF32 {
+    LinF32 router;
+    std::vector<LinF32> gate, up, down;  // per expert
+    bool has_dense = false;
+    LinF32 dgate, dup, ddown;
+};
+
+class MoeLayer {
+public:
+    MoeLayer(const nomas_moe_config& cfg, int64_t dim, int64_t hidden, DType dt, int device);
+    ~MoeLayer();
+    MoeLayer(const MoeLayer&) = delete;
+    MoeLayer& operator=(const MoeLayer&) = delete;
+
+    // Checks config and shape support before anything touches the GPU.
+    static int check_shape(const nomas_moe_config& cfg, int64_t dim, int64_t hidden, int dtype);
+
+    // Uploads parameters given as host arrays in the model dtype (reference
+    // layout).  Any bias may be null (zero).  Packs for the GEMM path.
+    int upload(const void* router_w, const void* gate_w, const void* gate_b, const void* up_w,
+               const void* up_b, const void* down_w, const void* down_b, const void* dg_w,
+               const void* dg_b, const void* du_w, const void* du_b, const void* dd_w,
+               const void* dd_b);
+    // Rounds f32 parameters to the model dtype and uploads them.
+    int upload_f32(const MoeParamsF32& p);
+
+    int forward(const void* x, void* y, int64_t rows, hipStream_t s);
+    int forward_host(const void* x, void* y, int64_t rows);
+    int routing(int32_t* idx, float* w, int32_t* counts, float* gap);
+    int set_profiling(bool on);
+    int stage_times(float* ms6);
+
+    int64_t n_params() const;
+    int64_t dim() const { return D_; }
+    int64_t hidden() const { return H_; }
+    int64_t experts() const { return E_; }
+    int64_t top_k() const { return k_; }
+    DType dtype() const { return dt_; }
+    bool uses_mfma() const { return mfma_; }
+
+private:
+    int ensure_workspace(int64_t rows);
+    void free_workspace();
+    int max_tiles(int64_t rows) const;
+
+    int64_t D_, H_, E_, k_;
+    int64_t Ecols_, kslots_;  // with the shared dense branch: E + 1, k + 1
+    double shared_dense_;
+    DType dt_;
+    int device_;
+    bool mfma_;
+    int BM_;
+
+    // device weights
+    void* d_wr_ = nullptr;
+    void* d_w1_ = nullptr;    // gate/up: MFMA packed [Ecols][2H][D], else [Ecols][2][H][D]
+    float* d_b1_ = nullptr;   // matching layout, f32
+    void* d_w2_ = nullptr;    // down [Ecols][D][H]
+    float* d_b2_ = nullptr;   // [Ecols][D]
+
+    // workspace (sized for cap_rows_)
+    int64_t cap_rows_ = 0;
+    void* d_ws_ = nullptr;
+    int32_t* d_idx_ = nullptr;
+    float* d_w_ = nullptr;
+    float* d_gap_ = nullptr;
+    int32_t* d_pos_ = nullptr;
+    int32_t* d_chunk_counts_ = nullptr;
+    int32_t* d_chunk_base_ = nullptr;
+    int32_t* d_expert_count_ = nullptr;
+    int32_t* d_expert_off_ = nullptr;
+    TileInfo* d_tiles_ = nullptr;
+    int32_t* d_tile_total_ = nullptr;
+    void* d_xperm_ = nullptr;
+    void* d_h_ = nullptr;
+    void* d_yperm_ = nullptr;
+
+    int64_t last_rows_ = -1;
+    hipStream_t last_stream_ = nullptr;
+
+    // profiling: one set of 7 events per recorded forward
+    bool profiling_ = false;
+    static constexpr int kRing = 512;
+    std::vector<hipEvent_t> events_;
+    int recorded_ = 0;
+};
+
+}  // namespace nomas

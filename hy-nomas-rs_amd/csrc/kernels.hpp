@@ -1,0 +1,97 @@
+// Host-side launch interface of the MoE feed-forward kernels.
+//
+// Pipeline of one forward (all on one stream):
+//   router  -> topk_idx / topk_w / gap per row, per-chunk expert histogram
+//   scan    -> per-chunk bases, expert counts/offsets, GEMM tile table
+//   dispatch-> stable permutation (tok_pos) + gather of x rows (x_perm)
+//   gemm_gate_up -> h = silu(x W_gate^T + b_gate) * (x W_up^T + b_up)
+//   gemm_down    -> y_perm = h W_down^T + b_down
+//   combine -> out[t] = sum over the row's slots (ascending expert) of w * y_perm
+#pragma once
+
+#include "common.hpp"
+
+namespace nomas {
+
+constexpr int kMaxExperts = 256;  // router LDS holds 64 rows x E f64 logits
+
+// Tile height (token rows) of the MFMA and of the general grouped GEMM.
+constexpr int kMfmaBM = 256;
+constexpr int kMfmaBN = 256;
+constexpr int kSimtBM = 64;
+
+struct RouterArgs {
+    const void* x;
+    const void* wr;
+    int64_t rows;
+    int D, E, k;
+    int k_slots;        // k, or k + 1 with the shared dense slot
+    float dense_coef;   // gate of the dense slot
+    int32_t* topk_idx;  // rows x k_slots
+    float* topk_w;      // rows x k_slots
+    float* gap;         // rows
+    int32_t* chunk_counts;  // nchunks x E_cols
+};
+
+struct ScanArgs {
+    const int32_t* chunk_counts;  // nchunks x E_cols
+    int nchunks;
+    int E_cols;
+    int BM;
+    int max_tiles;
+    int32_t* chunk_base;    // nchunks x E_cols
+    int32_t* expert_count;  // E_cols
+    int32_t* expert_off;    // E_cols + 1
+    TileInfo* tiles;        // max_tiles
+    int32_t* tile_total;    // 1
+};
+
+struct DispatchArgs {
+    const void* x;
+    int64_t rows;
+    int D, E_cols, k_slots;
+    const int32_t* topk_idx;
+    const int32_t* chunk_base;
+    int32_t* tok_pos;  // rows x k_slots
+    void* x_perm;      // A x D
+    int64_t a_cap;     // rows of x_perm (positions must stay below)
+};
+
+struct GemmArgs {
+    const void* X;     // token rows (A x K), expert-contiguous
+    const void* W;     // expert weights
+    const float* bias; // expert biases (f32)
+    void* out;
+    const TileInfo* tiles;
+    const int32_t* tile_total;
+    int max_tiles;
+    int N;  // output columns of the weight GEMM (2H for gate/up, D for down)
+    int K;
+    int num_experts;  // experts with weights (tiles naming others are skipped)
+    int64_t a_cap;    // rows of X / out (tiles reaching beyond are skipped)
+};
+
+struct CombineArgs {
+    const void* y_perm;
+    const int32_t* tok_pos;
+    const float* topk_w;
+    int64_t rows;
+    int D, k_slots;
+    void* out;
+    int64_t a_cap;  // rows of y_perm
+};
+
+size_t router_lds_bytes(int E);
+
+hipError_t launch_router(DType dt, const RouterArgs& a, hipStream_t s);
+hipError_t launch_scan(const ScanArgs& a, hipStream_t s);
+hipError_t launch_dispatch(DType dt, const DispatchArgs& a, hipStream_t s);
+// MFMA grouped GEMMs (bf16 / f16): W packed as described in moe_layer.cpp.
+hipError_t launch_gemm_gate_up_mfma(DType dt, const GemmArgs& a, hipStream_t s);
+hipError_t launch_gemm_down_mfma(DType dt, const GemmArgs& a, hipStream_t s);
+// General grouped GEMMs (any dtype, any shape).
+hipError_t launch_gemm_gate_up_simt(DType dt, const GemmArgs& a, hipStream_t s);
+hipError_t launch_gemm_down_simt(DType dt, const GemmArgs& a, hipStream_t s);
+hipError_t launch_combine(DType dt, const CombineArgs& a, hipStream_t s);
+
+}  // namespace nomas

@@ -1,0 +1,500 @@
+// MoeLayer: the object behind the C ABI (hy-nomas-rs modules/moe.rs:16-115).
+//
+// Owns the device copies of the router and expert parameters and a workspace
+// sized for the largest row count seen, and runs the six-stage forward
+// (router, scan, dispatch, gate/up GEMM, down GEMM, combine) on the caller's
+// stream.  The reference's dense evaluation (every expert on every row) and
+// this sparse evaluation give the same result: the reference multiplies the
+// rows of unselected experts by a zero gate (moe.rs:3-7,97-102).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "host.hpp"
+
+namespace nomas {
+
+// ---- errors ---------------------------------------------------------------
+
+namespace {
+thread_local std::string g_last_error;
+
+struct DeviceGuard {
+    int prev = -1;
+    bool ok = false;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        ok = hipSetDevice(dev) == hipSuccess;
+    }
+    ~DeviceGuard() {
+        if (prev >= 0) (void)hipSetDevice(prev);
+    }
+};
+
+inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+}  // namespace
+
+int set_error(int code, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+const char* last_error() { return g_last_error.c_str(); }
+void clear_error() { g_last_error.clear(); }
+
+#define HIP_TRY(expr)                                                                        \
+    do {                                                                                     \
+        hipError_t _e = (expr);                                                              \
+        if (_e != hipSuccess)                                                                \
+            return set_error(_e == hipErrorOutOfMemory ? NOMAS_ERR_OUT_OF_MEMORY : NOMAS_ERR_HIP, \
+                             "%s failed: %s", #expr, hipGetErrorString(_e));                 \
+    } while (0)
+
+// ---- construction ---------------------------------------------------------
+
+int MoeLayer::check_shape(const nomas_moe_config& cfg, int64_t dim, int64_t hidden, int dtype) {
+    if (cfg.experts < 1 || cfg.top_k < 1 || cfg.top_k > cfg.experts)
+        return set_error(NOMAS_ERR_INVALID_CONFIG, "invalid MoE top_k/experts (top_k=%lld, experts=%lld)",
+                         (long long)cfg.top_k, (long long)cfg.experts);
+    if (cfg.experts > kMaxExperts)
+        return set_error(NOMAS_ERR_INVALID_CONFIG, "experts=%lld exceeds the supported maximum %d",
+                         (long long)cfg.experts, kMaxExperts);
+    if (dtype < 0 || dtype > 2)
+        return set_error(NOMAS_ERR_INVALID_CONFIG, "unknown dtype code %d", dtype);
+    if (dim < 8 || dim % 8 != 0)
+        return set_error(NOMAS_ERR_INVALID_CONFIG,
+                         "dim=%lld must be a positive multiple of 8 (16-byte rows)", (long long)dim);
+    if (hidden < 1)
+        return set_error(NOMAS_ERR_INVALID_CONFIG, "hidden=%lld must be positive", (long long)hidden);
+    if (dim > (1 << 24) || hidden > (1 << 24))
+        return set_error(NOMAS_ERR_INVALID_CONFIG, "dim/hidden beyond the supported range");
+    return NOMAS_OK;
+}
+
+MoeLayer::MoeLayer(const nomas_moe_config& cfg, int64_t dim, int64_t hidden, DType dt, int device)
+    : D_(dim), H_(hidden), E_(cfg.experts), k_(cfg.top_k), shared_dense_(cfg.shared_dense),
+      dt_(dt), device_(device) {
+    const bool dense = cfg.shared_dense > 0.0;
+    Ecols_ = E_ + (dense ? 1 : 0);
+    kslots_ = k_ + (dense ? 1 : 0);
+    mfma_ = dt_ != DType::F32 && D_ % kMfmaBN == 0 && H_ % (kMfmaBN / 2) == 0;
+    BM_ = mfma_ ? kMfmaBM : kSimtBM;
+}
+
+MoeLayer::~MoeLayer() {
+    DeviceGuard g(device_);
+    free_workspace();
+    for (void* p : {d_wr_, d_w1_, (void*)d_b1_, d_w2_, (void*)d_b2_})
+        if (p) (void)hipFree(p);
+    for (hipEvent_t e : events_) (void)hipEventDestroy(e);
+}
+
+int64_t MoeLayer::n_params() const {
+    // router (no bias) + experts (gate, up, down with biases); dense excluded (moe.rs:112-114).
+    return E_ * D_ + E_ * (2 * (H_ * D_ + H_) + (D_ * H_ + D_));
+}
+
+int MoeLayer::upload(const void* router_w, const void* gate_w, const void* gate_b,
+                     const void* up_w, const void* up_b, const void* down_w, const void* down_b,
+                     const void* dg_w, const void* dg_b, const void* du_w, const void* du_b,
+                     const void* dd_w, const void* dd_b) {
+    if (!router_w || !gate_w || !up_w || !down_w)
+        return set_error(NOMAS_ERR_INVALID_ARGUMENT, "router/gate/up/down weights must be non-null");
+    const bool dense = Ecols_ > E_;
+    if (dense && (!dg_w || !du_w || !dd_w))
+        return set_error(NOMAS_ERR_INVALID_ARGUMENT,
+                         "shared_dense > 0 needs the dense gate/up/down weights");
+    const size_t es = dtype_size(dt_);
+    const int64_t D = D_, H = H_;
+    auto to_f32 = [&](const void* p, int64_t i) -> float {
+        const uint8_t* b = static_cast<const uint8_t*>(p) + i * es;
+        if (dt_ == DType::F32) { float f; std::memcpy(&f, b, 4); return f; }
+        uint16_t h;
+        std::memcpy(&h, b, 2);
+        return dt_ == DType::BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+    };
+    // Per-expert source pointers (dense branch appended as the last expert).
+    auto wsrc = [&](const void* moe, const void* dn, int64_t e, int64_t per) -> const uint8_t* {
+        if (e < E_) return static_cast<const uint8_t*>(moe) + e * per * es;
+        return static_cast<const uint8_t*>(dn);
+    };
+    auto bsrc = [&](const void* moe, const void* dn, int64_t e, int64_t per, int64_t i) -> float {
+        const void* base = e < E_ ? moe : dn;
+        if (!base) return 0.0f;
+        return to_f32(base, (e < E_ ? e * per : 0) + i);
+    };
+
+    DeviceGuard g(device_);
+    if (!g.ok) return set_error(NOMAS_ERR_HIP, "hipSetDevice(%d) failed", device_);
+
+    // gate/up
+    std::vector<uint8_t> w1((size_t)(Ecols_ * 2 * H * D) * es);
+    std::vector<float> b1((size_t)(Ecols_ * 2 * H));
+    for (int64_t e = 0; e < Ecols_; ++e) {
+        const uint8_t* gw = wsrc(gate_w, dg_w, e, H * D);
+        const uint8_t* uw = wsrc(up_w, du_w, e, H * D);
+        for (int64_t p = 0; p < 2 * H; ++p) {
+            int64_t src_row;
+            bool is_up;
+            if (mfma_) {  // rows 64g..64g+31 gate 32g.., rows 64g+32.. up 32g..
+                const int64_t grp = p / 64, w = p % 64;
+                is_up = w >= 32;
+                src_row = grp * 32 + (w % 32);
+            } else {      // [gate rows][up rows]
+                is_up = p >= H;
+                src_row = p % H;
+            }
+            const uint8_t* src = (is_up ? uw : gw) + src_row * D * es;
+            std::memcpy(&w1[(size_t)((e * 2 * H + p) * D) * es], src, (size_t)D * es);
+            b1[(size_t)(e * 2 * H + p)] = is_up ? bsrc(up_b, du_b, e, H, src_row)
+                                                : bsrc(gate_b, dg_b, e, H, src_row);
+        }
+    }
+    // down
+    std::vector<uint8_t> w2((size_t)(Ecols_ * D * H) * es);
+    std::vector<float> b2((size_t)(Ecols_ * D));
+    for (int64_t e = 0; e < Ecols_; ++e) {
+        std::memcpy(&w2[(size_t)(e * D * H) * es], wsrc(down_w, dd_w, e, D * H), (size_t)(D * H) * es);
+        for (int64_t d = 0; d < D; ++d) b2[(size_t)(e * D + d)] = bsrc(down_b, dd_b, e, D, d);
+    }
+
+    for (void* p : {d_wr_, d_w1_, (void*)d_b1_, d_w2_, (void*)d_b2_})
+        if (p) (void)hipFree(p);
+    d_wr_ = d_w1_ = d_w2_ = nullptr;
+    d_b1_ = d_b2_ = nullptr;
+    HIP_TRY(hipMalloc(&d_wr_, (size_t)(E_ * D) * es));
+    HIP_TRY(hipMalloc(&d_w1_, w1.size()));
+    HIP_TRY(hipMalloc((void**)&d_b1_, b1.size() * sizeof(float)));
+    HIP_TRY(hipMalloc(&d_w2_, w2.size()));
+    HIP_TRY(hipMalloc((void**)&d_b2_, b2.size() * sizeof(float)));
+    HIP_TRY(hipMemcpy(d_wr_, router_w, (size_t)(E_ * D) * es, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(d_w1_, w1.data(), w1.size(), hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(d_b1_, b1.data(), b1.size() * sizeof(float), hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(d_w2_, w2.data(), w2.size(), hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(d_b2_, b2.data(), b2.size() * sizeof(float), hipMemcpyHostToDevice));
+    return NOMAS_OK;
+}
+
+int MoeLayer::upload_f32(const MoeParamsF32& p) {
+    const size_t es = dtype_size(dt_);
+    auto cvt = [&](const std::vector<float>& v, std::vector<uint8_t>* out) {
+        out->resize(v.size() * es);
+        if (dt_ == DType::F32) {
+            std::memcpy(out->data(), v.data(), v.size() * 4);
+            return;
+        }
+        uint16_t* o = reinterpret_cast<uint16_t*>(out->data());
+        for (size_t i = 0; i < v.size(); ++i)
+            o[i] = dt_ == DType::BF16 ? f32_to_bf16_bits(v[i]) : f32_to_f16_bits(v[i]);
+    };
+    auto cat = [&](const std::vector<LinF32>& ls, bool bias, int64_t per) {
+        std::vector<float> all;
+        all.reserve(ls.size() * per);
+        for (const LinF32& l : ls) {
+            const std::vector<float>& src = bias ? l.b : l.w;
+            if (src.empty()) all.insert(all.end(), per, 0.0f);
+            else all.insert(all.end(), src.begin(), src.end());
+        }
+        return all;
+    };
+    const int64_t D = D_, H = H_;
+    std::vector<uint8_t> r, gw, gb, uw, ub, dw, db, xgw, xgb, xuw, xub, xdw, xdb;
+    cvt(p.router.w, &r);
+    cvt(cat(p.gate, false, H * D), &gw);
+    cvt(cat(p.gate, true, H), &gb);
+    cvt(cat(p.up, false, H * D), &uw);
+    cvt(cat(p.up, true, H), &ub);
+    cvt(cat(p.down, false, D * H), &dw);
+    cvt(cat(p.down, true, D), &db);
+    const bool dense = Ecols_ > E_ && p.has_dense;
+    if (dense) {
+        cvt(p.dgate.w, &xgw);
+        cvt(p.dgate.b.empty() ? std::vector<float>(H, 0.0f) : p.dgate.b, &xgb);
+        cvt(p.dup.w, &xuw);
+        cvt(p.dup.b.empty() ? std::vector<float>(H, 0.0f) : p.dup.b, &xub);
+        cvt(p.ddown.w, &xdw);
+        cvt(p.ddown.b.empty() ? std::vector<float>(D, 0.0f) : p.ddown.b, &xdb);
+    }
+    return upload(r.data(), gw.data(), gb.data(), uw.data(), ub.data(), dw.data(), db.data(),
+                  dense ? xgw.data() : nullptr, dense ? xgb.data() : nullptr,
+                  dense ? xuw.data() : nullptr, dense ? xub.data() : nullptr,
+                  dense ? xdw.data() : nullptr, dense ? xdb.data() : nullptr);
+}
+
+// ---- workspace --------------------------------------------------------------
+
+int MoeLayer::max_tiles(int64_t rows) const {
+    const int64_t A = rows * kslots_;
+    return (int)((A + BM_ - 1) / BM_ + Ecols_);
+}
+
+void MoeLayer::free_workspace() {
+    if (d_ws_) (void)hipFree(d_ws_);
+    d_ws_ = nullptr;
+    cap_rows_ = 0;
+}
+
+int MoeLayer::ensure_workspace(int64_t rows) {
+    if (rows <= cap_rows_) return NOMAS_OK;
+    int64_t cap = std::max<int64_t>(rows, cap_rows_ + cap_rows_ / 2);
+    cap = (cap + kRouterRows - 1) / kRouterRows * kRouterRows;
+    const int64_t A = cap * kslots_;
+    const int64_t nch = cap / kRouterRows;
+    const size_t es = dtype_size(dt_);
+    const int mt = max_tiles(cap);
+    size_t off = 0;
+    auto take = [&](size_t bytes) { size_t o = off; off += align256(bytes); return o; };
+    const size_t o_idx = take(sizeof(int32_t) * A);
+    const size_t o_w = take(sizeof(float) * A);
+    const size_t o_gap = take(sizeof(float) * cap);
+    const size_t o_pos = take(sizeof(int32_t) * A);
+    const size_t o_cc = take(sizeof(int32_t) * nch * Ecols_);
+    const size_t o_cb = take(sizeof(int32_t) * nch * Ecols_);
+    const size_t o_ec = take(sizeof(int32_t) * Ecols_);
+    const size_t o_eo = take(sizeof(int32_t) * (Ecols_ + 1));
+    const size_t o_tiles = take(sizeof(TileInfo) * mt);
+    const size_t o_tt = take(sizeof(int32_t));
+    const size_t o_xp = take(es * A * D_);
+    const size_t o_h = take(es * A * H_);
+    const size_t o_yp = take(es * A * D_);
+    free_workspace();
+    void* ws = nullptr;
+    HIP_TRY(hipMalloc(&ws, off));
+    d_ws_ = ws;
+    uint8_t* b = static_cast<uint8_t*>(ws);
+    d_idx_ = reinterpret_cast<int32_t*>(b + o_idx);
+    d_w_ = reinterpret_cast<float*>(b + o_w);
+    d_gap_ = reinterpret_cast<float*>(b + o_gap);
+    d_pos_ = reinterpret_cast<int32_t*>(b + o_pos);
+    d_chunk_counts_ = reinterpret_cast<int32_t*>(b + o_cc);
+    d_chunk_base_ = reinterpret_cast<int32_t*>(b + o_cb);
+    d_expert_count_ = reinterpret_cast<int32_t*>(b + o_ec);
+    d_expert_off_ = reinterpret_cast<int32_t*>(b + o_eo);
+    d_tiles_ = reinterpret_cast<TileInfo*>(b + o_tiles);
+    d_tile_total_ = reinterpret_cast<int32_t*>(b + o_tt);
+    d_xperm_ = b + o_xp;
+    d_h_ = b + o_h;
+    d_yperm_ = b + o_yp;
+    cap_rows_ = cap;
+    return NOMAS_OK;
+}
+
+// ---- forward ------------------------------------------------------------------
+
+int MoeLayer::forward(const void* x, void* y, int64_t rows, hipStream_t s) {
+    if (rows < 0) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "rows must be >= 0 (got %lld)", (long long)rows);
+    if (rows == 0) { last_rows_ = 0; return NOMAS_OK; }
+    if (!x || !y) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "x and y must be non-null");
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15)
+        return set_error(NOMAS_ERR_INVALID_ARGUMENT, "x and y must be 16-byte aligned");
+    if (!d_w1_) return set_error(NOMAS_ERR_STATE, "weights have not been uploaded");
+    if (rows * kslots_ > 0x7fffffffLL || rows * kslots_ * std::max(D_, H_) > (1LL << 40))
+        return set_error(NOMAS_ERR_INVALID_ARGUMENT, "rows=%lld exceed the supported range", (long long)rows);
+    DeviceGuard g(device_);
+    if (!g.ok) return set_error(NOMAS_ERR_HIP, "hipSetDevice(%d) failed", device_);
+    int rc = ensure_workspace(rows);
+    if (rc != NOMAS_OK) return rc;
+
+    const int nch = (int)((rows + kRouterRows - 1) / kRouterRows);
+    const int mt = max_tiles(rows);
+    hipEvent_t* ev = nullptr;
+    if (profiling_) {
+        ev = &events_[(size_t)(recorded_ % kRing) * 7];
+        ++recorded_;
+    }
+    auto mark = [&](int i) -> int {
+        if (ev) HIP_TRY(hipEventRecord(ev[i], s));
+        return NOMAS_OK;
+    };
+#define STAGE(call, what)                                                                  \
+    do {                                                                                   \
+        hipError_t _e = (call);                                                            \
+        if (_e != hipSuccess)                                                              \
+            return set_error(NOMAS_ERR_HIP, "%s launch failed: %s", what, hipGetErrorString(_e)); \
+    } while (0)
+
+    if ((rc = mark(0))) return rc;
+    RouterArgs ra;
+    ra.x = x;
+    ra.wr = d_wr_;
+    ra.rows = rows;
+    ra.D = (int)D_;
+    ra.E = (int)E_;
+    ra.k = (int)k_;
+    ra.k_slots = (int)kslots_;
+    ra.dense_coef = (float)shared_dense_;
+    ra.topk_idx = d_idx_;
+    ra.topk_w = d_w_;
+    ra.gap = d_gap_;
+    ra.chunk_counts = d_chunk_counts_;
+    STAGE(launch_router(dt_, ra, s), "router");
+    if ((rc = mark(1))) return rc;
+
+    ScanArgs sa;
+    sa.chunk_counts = d_chunk_counts_;
+    sa.nchunks = nch;
+    sa.E_cols = (int)Ecols_;
+    sa.BM = BM_;
+    sa.max_tiles = mt;
+    sa.chunk_base = d_chunk_base_;
+    sa.expert_count = d_expert_count_;
+    sa.expert_off = d_expert_off_;
+    sa.tiles = d_tiles_;
+    sa.tile_total = d_tile_total_;
+    STAGE(launch_scan(sa, s), "scan");
+    if ((rc = mark(2))) return rc;
+
+    DispatchArgs da;
+    da.x = x;
+    da.rows = rows;
+    da.D = (int)D_;
+    da.E_cols = (int)Ecols_;
+    da.k_slots = (int)kslots_;
+    da.topk_idx = d_idx_;
+    da.chunk_base = d_chunk_base_;
+    da.tok_pos = d_pos_;
+    da.x_perm = d_xperm_;
+    da.a_cap = cap_rows_ * kslots_;
+    STAGE(launch_dispatch(dt_, da, s), "dispatch");
+    if ((rc = mark(3))) return rc;
+
+    GemmArgs g1;
+    g1.X = d_xperm_;
+    g1.W = d_w1_;
+    g1.bias = d_b1_;
+    g1.out = d_h_;
+    g1.tiles = d_tiles_;
+    g1.tile_total = d_tile_total_;
+    g1.max_tiles = mt;
+    g1.N = (int)(2 * H_);
+    g1.K = (int)D_;
+    g1.num_experts = (int)Ecols_;
+    g1.a_cap = cap_rows_ * kslots_;
+    STAGE(mfma_ ? launch_gemm_gate_up_mfma(dt_, g1, s) : launch_gemm_gate_up_simt(dt_, g1, s),
+          "gate/up GEMM");
+    if ((rc = mark(4))) return rc;
+
+    GemmArgs g2 = g1;
+    g2.X = d_h_;
+    g2.W = d_w2_;
+    g2.bias = d_b2_;
+    g2.out = d_yperm_;
+    g2.N = (int)D_;
+    g2.K = (int)H_;
+    STAGE(mfma_ ? launch_gemm_down_mfma(dt_, g2, s) : launch_gemm_down_simt(dt_, g2, s),
+          "down GEMM");
+    if ((rc = mark(5))) return rc;
+
+    CombineArgs ca;
+    ca.y_perm = d_yperm_;
+    ca.tok_pos = d_pos_;
+    ca.topk_w = d_w_;
+    ca.rows = rows;
+    ca.D = (int)D_;
+    ca.k_slots = (int)kslots_;
+    ca.out = y;
+    ca.a_cap = cap_rows_ * kslots_;
+    STAGE(launch_combine(dt_, ca, s), "combine");
+    if ((rc = mark(6))) return rc;
+#undef STAGE
+    last_rows_ = rows;
+    last_stream_ = s;
+    return NOMAS_OK;
+}
+
+int MoeLayer::forward_host(const void* x, void* y, int64_t rows) {
+    if (rows < 0) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "rows must be >= 0");
+    if (rows == 0) { last_rows_ = 0; return NOMAS_OK; }
+    if (!x || !y) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "x and y must be non-null");
+    DeviceGuard g(device_);
+    if (!g.ok) return set_error(NOMAS_ERR_HIP, "hipSetDevice(%d) failed", device_);
+    const size_t bytes = (size_t)(rows * D_) * dtype_size(dt_);
+    void *dx = nullptr, *dy = nullptr;
+    HIP_TRY(hipMalloc(&dx, bytes));
+    hipError_t e = hipMalloc(&dy, bytes);
+    if (e != hipSuccess) {
+        (void)hipFree(dx);
+        return set_error(NOMAS_ERR_OUT_OF_MEMORY, "hipMalloc of the output failed: %s", hipGetErrorString(e));
+    }
+    int rc = NOMAS_OK;
+    e = hipMemcpy(dx, x, bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) rc = set_error(NOMAS_ERR_HIP, "hipMemcpy H2D failed: %s", hipGetErrorString(e));
+    if (rc == NOMAS_OK) rc = forward(dx, dy, rows, nullptr);
+    if (rc == NOMAS_OK) {
+        e = hipMemcpy(y, dy, bytes, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) rc = set_error(NOMAS_ERR_HIP, "hipMemcpy D2H failed: %s", hipGetErrorString(e));
+    }
+    (void)hipFree(dx);
+    (void)hipFree(dy);
+    return rc;
+}
+
+int MoeLayer::routing(int32_t* idx, float* w, int32_t* counts, float* gap) {
+    if (last_rows_ < 0) return set_error(NOMAS_ERR_STATE, "no forward has run on this handle");
+    DeviceGuard g(device_);
+    HIP_TRY(hipStreamSynchronize(last_stream_));
+    const int64_t rows = last_rows_;
+    if (rows == 0) {
+        if (counts) std::memset(counts, 0, sizeof(int32_t) * E_);
+        return NOMAS_OK;
+    }
+    if (idx || w) {
+        std::vector<int32_t> hi((size_t)(rows * kslots_));
+        std::vector<float> hw((size_t)(rows * kslots_));
+        HIP_TRY(hipMemcpy(hi.data(), d_idx_, hi.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
+        HIP_TRY(hipMemcpy(hw.data(), d_w_, hw.size() * sizeof(float), hipMemcpyDeviceToHost));
+        for (int64_t r = 0; r < rows; ++r)
+            for (int64_t j = 0; j < k_; ++j) {
+                if (idx) idx[r * k_ + j] = hi[(size_t)(r * kslots_ + j)];
+                if (w) w[r * k_ + j] = hw[(size_t)(r * kslots_ + j)];
+            }
+    }
+    if (counts) HIP_TRY(hipMemcpy(counts, d_expert_count_, sizeof(int32_t) * E_, hipMemcpyDeviceToHost));
+    if (gap) HIP_TRY(hipMemcpy(gap, d_gap_, sizeof(float) * rows, hipMemcpyDeviceToHost));
+    return NOMAS_OK;
+}
+
+int MoeLayer::set_profiling(bool on) {
+    DeviceGuard g(device_);
+    if (on && events_.empty()) {
+        events_.resize((size_t)kRing * 7);
+        for (hipEvent_t& e : events_) HIP_TRY(hipEventCreate(&e));
+    }
+    profiling_ = on;
+    recorded_ = 0;
+    return NOMAS_OK;
+}
+
+int MoeLayer::stage_times(float* ms6) {
+    if (!ms6) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "ms6 must be non-null");
+    if (!profiling_ || recorded_ == 0)
+        return set_error(NOMAS_ERR_STATE, "no profiled forward recorded");
+    DeviceGuard g(device_);
+    const int n = std::min(recorded_, kRing);
+    double sum[6] = {0, 0, 0, 0, 0, 0};
+    for (int i = 0; i < n; ++i) {
+        const int set = (recorded_ - 1 - i) % kRing;
+        hipEvent_t* ev = &events_[(size_t)set * 7];
+        HIP_TRY(hipEventSynchronize(ev[6]));
+        for (int st = 0; st < 6; ++st) {
+            float ms = 0.0f;
+            HIP_TRY(hipEventElapsedTime(&ms, ev[st], ev[st + 1]));
+            sum[st] += ms;
+        }
+    }
+    for (int st = 0; st < 6; ++st) ms6[st] = (float)(sum[st] / n);
+    recorded_ = 0;
+    return NOMAS_OK;
+}
+
+}  // namespace nomas

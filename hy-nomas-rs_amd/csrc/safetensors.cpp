@@ -1,0 +1,267 @@
+// Minimal safetensors reader for the MoE parameters (the format candle's
+// safetensors::load reads in weights.rs:113-116): an 8-byte little-endian
+// header length, a JSON header mapping tensor names to
+// {"dtype", "shape", "data_offsets": [begin, end]}, then the payload.
+// Only the requested tensors are read from disk.
+#include <cstdio>
+#include <cstring>
+
+#include "host.hpp"
+
+namespace nomas {
+
+namespace {
+
+struct Entry {
+    std::string dtype;
+    std::vector<int64_t> shape;
+    int64_t begin = -1, end = -1;
+};
+
+// Tiny recursive-descent JSON parser covering the safetensors header.
+class Json {
+public:
+    explicit Json(const std::string& s) : s_(s) {}
+
+    bool parse_header(std::map<std::string, Entry>* out) {
+        ws();
+        if (!eat('{')) return false;
+        ws();
+        if (eat('}')) return true;
+        for (;;) {
+            std::string key;
+            ws();
+            if (!str(&key)) return false;
+            ws();
+            if (!eat(':')) return false;
+            ws();
+            if (key == "__metadata__") {
+                if (!skip()) return false;
+            } else {
+                Entry e;
+                if (!entry(&e)) return false;
+                (*out)[key] = e;
+            }
+            ws();
+            if (eat(',')) continue;
+            if (eat('}')) return true;
+            return false;
+        }
+    }
+
+private:
+    const std::string& s_;
+    size_t p_ = 0;
+
+    void ws() {
+        while (p_ < s_.size() && (s_[p_] == ' ' || s_[p_] == '\n' || s_[p_] == '\t' || s_[p_] == '\r'))
+            ++p_;
+    }
+    bool eat(char c) {
+        if (p_ < s_.size() && s_[p_] == c) { ++p_; return true; }
+        return false;
+    }
+    bool str(std::string* out) {
+        if (!eat('"')) return false;
+        out->clear();
+        while (p_ < s_.size() && s_[p_] != '"') {
+            if (s_[p_] == '\\') {
+                ++p_;
+                if (p_ >= s_.size()) return false;
+                const char c = s_[p_];
+                if (c == 'u') {  // keep escaped code points verbatim; tensor names are ASCII
+                    if (p_ + 4 >= s_.size()) return false;
+                    out->append(s_, p_ - 1, 6);
+                    p_ += 5;
+                    continue;
+                }
+                out->push_back(c == 'n' ? '\n' : c == 't' ? '\t' : c);
+                ++p_;
+            } else {
+                out->push_back(s_[p_++]);
+            }
+        }
+        return eat('"');
+    }
+    bool integer(int64_t* v) {
+        ws();
+        size_t q = p_;
+        bool neg = false;
+        if (q < s_.size() && s_[q] == '-') { neg = true; ++q; }
+        if (q >= s_.size() || s_[q] < '0' || s_[q] > '9') return false;
+        int64_t x = 0;
+        while (q < s_.size() && s_[q] >= '0' && s_[q] <= '9') x = x * 10 + (s_[q++] - '0');
+        p_ = q;
+        *v = neg ? -x : x;
+        return true;
+    }
+    bool int_array(std::vector<int64_t>* v) {
+        ws();
+        if (!eat('[')) return false;
+        ws();
+        if (eat(']')) return true;
+        for (;;) {
+            int64_t x;
+            if (!integer(&x)) return false;
+            v->push_back(x);
+            ws();
+            if (eat(',')) continue;
+            if (eat(']')) return true;
+            return false;
+        }
+    }
+    bool entry(Entry* e) {
+        if (!eat('{')) return false;
+        for (;;) {
+            ws();
+            std::string k;
+            if (!str(&k)) return false;
+            ws();
+            if (!eat(':')) return false;
+            ws();
+            if (k == "dtype") {
+                if (!str(&e->dtype)) return false;
+            } else if (k == "shape") {
+                if (!int_array(&e->shape)) return false;
+            } else if (k == "data_offsets") {
+                std::vector<int64_t> o;
+                if (!int_array(&o) || o.size() != 2) return false;
+                e->begin = o[0];
+                e->end = o[1];
+            } else if (!skip()) {
+                return false;
+            }
+            ws();
+            if (eat(',')) continue;
+            if (eat('}')) return true;
+            return false;
+        }
+    }
+    bool skip() {  // any JSON value
+        ws();
+        if (p_ >= s_.size()) return false;
+        const char c = s_[p_];
+        if (c == '"') { std::string t; return str(&t); }
+        if (c == '{' || c == '[') {
+            const char close = c == '{' ? '}' : ']';
+            ++p_;
+            ws();
+            if (eat(close)) return true;
+            for (;;) {
+                ws();
+                if (c == '{') {
+                    std::string t;
+                    if (!str(&t)) return false;
+                    ws();
+                    if (!eat(':')) return false;
+                }
+                if (!skip()) return false;
+                ws();
+                if (eat(',')) continue;
+                if (eat(close)) return true;
+                return false;
+            }
+        }
+        while (p_ < s_.size() && s_[p_] != ',' && s_[p_] != '}' && s_[p_] != ']') ++p_;
+        return true;
+    }
+};
+
+int64_t dtype_bytes(const std::string& d) {
+    if (d == "F64" || d == "I64" || d == "U64") return 8;
+    if (d == "F32" || d == "I32" || d == "U32") return 4;
+    if (d == "BF16" || d == "F16" || d == "I16" || d == "U16") return 2;
+    if (d == "U8" || d == "I8" || d == "BOOL" || d == "F8_E4M3" || d == "F8_E5M2") return 1;
+    return -1;
+}
+
+}  // namespace
+
+int read_safetensors(const std::vector<std::string>& files, const std::vector<std::string>& names,
+                     std::map<std::string, StTensor>* out) {
+    for (const std::string& path : files) {
+        FILE* f = std::fopen(path.c_str(), "rb");
+        if (!f) return set_error(NOMAS_ERR_IO, "loading %s: cannot open file", path.c_str());
+        uint8_t hb[8];
+        if (std::fread(hb, 1, 8, f) != 8) {
+            std::fclose(f);
+            return set_error(NOMAS_ERR_IO, "loading %s: truncated header", path.c_str());
+        }
+        uint64_t hlen = 0;
+        for (int i = 7; i >= 0; --i) hlen = (hlen << 8) | hb[i];
+        if (hlen > (1ull << 30)) {
+            std::fclose(f);
+            return set_error(NOMAS_ERR_IO, "loading %s: header too large", path.c_str());
+        }
+        std::string hdr(hlen, '\0');
+        if (std::fread(&hdr[0], 1, hlen, f) != hlen) {
+            std::fclose(f);
+            return set_error(NOMAS_ERR_IO, "loading %s: truncated header", path.c_str());
+        }
+        std::map<std::string, Entry> entries;
+        Json js(hdr);
+        if (!js.parse_header(&entries)) {
+            std::fclose(f);
+            return set_error(NOMAS_ERR_IO, "loading %s: malformed safetensors header", path.c_str());
+        }
+        const int64_t data0 = 8 + (int64_t)hlen;
+        for (const std::string& n : names) {
+            auto it = entries.find(n);
+            if (it == entries.end()) continue;
+            const Entry& e = it->second;
+            const int64_t eb = dtype_bytes(e.dtype);
+            int64_t numel = 1;
+            for (int64_t d : e.shape) numel *= d;
+            if (eb < 0 || e.begin < 0 || e.end - e.begin != numel * eb) {
+                std::fclose(f);
+                return set_error(NOMAS_ERR_IO, "loading %s: bad entry for %s", path.c_str(), n.c_str());
+            }
+            StTensor t;
+            t.dtype = e.dtype;
+            t.shape = e.shape;
+            t.data.resize((size_t)(e.end - e.begin));
+            if (std::fseek(f, (long)(data0 + e.begin), SEEK_SET) != 0 ||
+                std::fread(t.data.data(), 1, t.data.size(), f) != t.data.size()) {
+                std::fclose(f);
+                return set_error(NOMAS_ERR_IO, "loading %s: truncated payload of %s", path.c_str(),
+                                 n.c_str());
+            }
+            (*out)[n] = std::move(t);
+        }
+        std::fclose(f);
+    }
+    return NOMAS_OK;
+}
+
+int st_to_f32(const StTensor& t, std::vector<float>* out) {
+    const size_t n = t.data.size() / (size_t)std::max<int64_t>(1, dtype_bytes(t.dtype));
+    out->resize(n);
+    const uint8_t* p = t.data.data();
+    if (t.dtype == "F32") {
+        std::memcpy(out->data(), p, n * 4);
+    } else if (t.dtype == "F64") {
+        for (size_t i = 0; i < n; ++i) {
+            double d;
+            std::memcpy(&d, p + 8 * i, 8);
+            (*out)[i] = (float)d;
+        }
+    } else if (t.dtype == "BF16") {
+        for (size_t i = 0; i < n; ++i) {
+            uint16_t b;
+            std::memcpy(&b, p + 2 * i, 2);
+            (*out)[i] = bf16_bits_to_f32(b);
+        }
+    } else if (t.dtype == "F16") {
+        for (size_t i = 0; i < n; ++i) {
+            uint16_t b;
+            std::memcpy(&b, p + 2 * i, 2);
+            (*out)[i] = f16_bits_to_f32(b);
+        }
+    } else {
+        return set_error(NOMAS_ERR_INVALID_ARGUMENT, "unsupported safetensors dtype %s",
+                         t.dtype.c_str());
+    }
+    return NOMAS_OK;
+}
+
+}  // namespace nomas

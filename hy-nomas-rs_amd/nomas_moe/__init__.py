@@ -1,0 +1,317 @@
+"""MI355X top-k MoE feed-forward block with hy-nomas-rs's module interface.
+
+Mirrors the reference's Rust API (nomas-core/src/modules/moe.rs,
+nomas-core/src/config.rs:202-213, nomas-core/src/modules/mod.rs:20-56):
+
+    cfg = MoeConfig(experts=4, top_k=2, shared_dense=0.0, seed=1)
+    moe = MoeLayer.from_source(Weights.random(4, DataType.F32), "blocks.0.moe", 32, 64, cfg)
+    y = moe.forward(x)          # x: (..., D) torch tensor on the GPU or the host
+    moe.n_params()
+
+Every computation runs in libnomas_moe.so (hand-written gfx950 kernels behind
+a C ABI); this module only marshals arguments.  Errors raise NomasError
+subclasses that mirror the reference's error variants (error.rs:7-46).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import enum
+from dataclasses import dataclass
+from typing import Mapping, Sequence
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import nomas_moe_config
+
+__all__ = [
+    "DataType", "MoeConfig", "Weights", "MoeLayer", "NomasError", "InvalidConfig", "WeightKey",
+    "IoError", "path_seed", "randn_affine", "to_model_dtype",
+]
+
+
+class DataType(enum.IntEnum):
+    """config.rs:30-39."""
+    F32 = 0
+    Bf16 = 1
+    F16 = 2
+
+    @property
+    def torch(self) -> torch.dtype:
+        return {0: torch.float32, 1: torch.bfloat16, 2: torch.float16}[int(self)]
+
+    @classmethod
+    def of(cls, dt) -> "DataType":
+        if isinstance(dt, DataType):
+            return dt
+        if isinstance(dt, torch.dtype):
+            return {torch.float32: cls.F32, torch.bfloat16: cls.Bf16, torch.float16: cls.F16}[dt]
+        return {"f32": cls.F32, "bf16": cls.Bf16, "f16": cls.F16}[str(dt).lower()]
+
+
+class NomasError(RuntimeError):
+    """A failed call into the library; ``code`` is the nomas_status value."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(msg)
+        self.code = code
+
+
+class InvalidConfig(NomasError):
+    """Error::InvalidConfig (error.rs:24-26)."""
+
+
+class WeightKey(NomasError):
+    """Error::WeightKey (error.rs:20-22)."""
+
+
+class IoError(NomasError):
+    """Error::Io (error.rs:12-14)."""
+
+
+_ERRORS = {1: InvalidConfig, 3: WeightKey, 4: IoError}
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise _ERRORS.get(rc, NomasError)(rc, _lib.last_error())
+
+
+@dataclass
+class MoeConfig:
+    """MoeConfig (config.rs:202-213)."""
+    experts: int
+    top_k: int
+    shared_dense: float = 0.0
+    seed: int = 0
+
+    def _c(self) -> nomas_moe_config:
+        return nomas_moe_config(int(self.experts), int(self.top_k), float(self.shared_dense),
+                                int(self.seed) & 0xFFFFFFFFFFFFFFFF)
+
+    def validate(self) -> None:
+        """The MoE clause of NomasConfig::validate (config.rs:394-399)."""
+        c = self._c()
+        _check(_lib.lib().nomas_moe_config_validate(C.byref(c)))
+
+
+def path_seed(seed: int, path: str) -> int:
+    """Weights::path_seed (mod.rs:47-55)."""
+    return int(_lib.lib().nomas_path_seed(seed & 0xFFFFFFFFFFFFFFFF, path.encode()))
+
+
+def randn_affine(seed: int, n: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    """deterministic_randn_affine (tensor_utils.rs:123-138), flattened, f32."""
+    out = np.empty(int(n), np.float32)
+    _lib.lib().nomas_randn_affine(seed & 0xFFFFFFFFFFFFFFFF, float(mean), float(std), int(n),
+                                  out.ctypes.data)
+    return out
+
+
+def to_model_dtype(a: np.ndarray, dtype) -> np.ndarray:
+    """f32 array -> raw storage of the model dtype (round to nearest even):
+    float32 for F32, uint16 bit patterns for Bf16 / F16."""
+    dt = DataType.of(dtype)
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    if dt == DataType.F32:
+        return a
+    out = np.empty(a.shape, np.uint16)
+    fn = _lib.lib().nomas_f32_to_bf16 if dt == DataType.Bf16 else _lib.lib().nomas_f32_to_f16
+    fn(a.ctypes.data, out.ctypes.data, a.size)
+    return out
+
+
+def widen(a: np.ndarray, dtype) -> np.ndarray:
+    """Raw model-dtype storage -> f32 values (exact)."""
+    dt = DataType.of(dtype)
+    if dt == DataType.F32:
+        return np.asarray(a, np.float32)
+    if dt == DataType.Bf16:
+        return (np.asarray(a, np.uint16).astype(np.uint32) << 16).view(np.float32)
+    return np.asarray(a, np.uint16).view(np.float16).astype(np.float32)
+
+
+class Weights:
+    """Where a module's parameters come from (mod.rs:20-45).
+
+    * ``Weights.random(seed, dtype)`` -- deterministic xavier init keyed by the
+      parameter path, zero biases (Weights::Random).
+    * ``Weights.loaded(files, dtype)`` -- safetensors checkpoint files
+      (Weights::Loaded over weights::load_dit's VarBuilder).
+    * ``Weights.tensors(mapping, dtype)`` -- in-memory f32 arrays keyed like
+      the checkpoint (VarBuilder::from_tensors).
+    """
+
+    def __init__(self, kind: str, dtype, device: int = 0, seed: int = 0,
+                 files: Sequence[str] = (), tensors: Mapping[str, np.ndarray] | None = None):
+        self.kind = kind
+        self.dtype = DataType.of(dtype)
+        self.device = int(device)
+        self.seed = int(seed)
+        self.files = list(files)
+        self.tensors = dict(tensors or {})
+
+    @classmethod
+    def random(cls, seed: int, dtype=DataType.F32, device: int = 0) -> "Weights":
+        return cls("random", dtype, device, seed=seed)
+
+    @classmethod
+    def loaded(cls, files: Sequence[str] | str, dtype=DataType.F32, device: int = 0) -> "Weights":
+        if isinstance(files, str):
+            files = [files]
+        return cls("loaded", dtype, device, files=files)
+
+    @classmethod
+    def tensors_(cls, tensors: Mapping[str, np.ndarray], dtype=DataType.F32,
+                 device: int = 0) -> "Weights":
+        return cls("tensors", dtype, device, tensors=tensors)
+
+    # the reference names this VarBuilder::from_tensors; keep a short alias
+    from_tensors = tensors_
+
+
+class MoeLayer:
+    """Router + expert bank (moe.rs:16-22) on one MI355X."""
+
+    def __init__(self, handle: C.c_void_p, cfg: MoeConfig, dtype: DataType, device: int):
+        self._h = handle
+        self.cfg = cfg
+        self.dtype = dtype
+        self.device = device
+        d, hdn, e, k, dt = C.c_int64(), C.c_int64(), C.c_int64(), C.c_int64(), C.c_int()
+        _check(_lib.lib().nomas_moe_dims(self._h, C.byref(d), C.byref(hdn), C.byref(e),
+                                         C.byref(k), C.byref(dt)))
+        self.dim, self.hidden, self.experts, self.top_k = d.value, hdn.value, e.value, k.value
+
+    # -- construction: MoeLayer::from_source (moe.rs:26-62) ------------------
+    @classmethod
+    def from_source(cls, src: Weights, path: str, dim: int, hidden: int,
+                    cfg: MoeConfig) -> "MoeLayer":
+        L = _lib.lib()
+        c = cfg._c()
+        h = C.c_void_p()
+        if src.kind == "random":
+            rc = L.nomas_moe_from_random(C.byref(c), path.encode(), dim, hidden, int(src.dtype),
+                                         src.seed & 0xFFFFFFFFFFFFFFFF, src.device, C.byref(h))
+        elif src.kind == "loaded":
+            arr = (C.c_char_p * len(src.files))(*[f.encode() for f in src.files])
+            rc = L.nomas_moe_from_safetensors(C.byref(c), arr, len(src.files), path.encode(), dim,
+                                              hidden, int(src.dtype), src.device, C.byref(h))
+        elif src.kind == "tensors":
+            rc = cls._from_tensors(src, path, dim, hidden, cfg, c, h)
+        else:
+            raise ValueError(f"unknown weight source {src.kind!r}")
+        _check(rc)
+        return cls(h, cfg, src.dtype, src.device)
+
+    @staticmethod
+    def _from_tensors(src, path, dim, hidden, cfg, c, h) -> int:
+        t = src.tensors
+        E = int(cfg.experts)
+
+        def stack(fmt, shape, bias):
+            arrs = []
+            for e in range(E):
+                key = fmt.format(e=e)
+                if key not in t:
+                    if bias:
+                        arrs.append(np.zeros(shape, np.float32))
+                        continue
+                    raise WeightKey(3, f"missing tensor {key}")
+                a = np.asarray(t[key], np.float32)
+                if a.shape != shape:
+                    raise WeightKey(3, f"{key}: expected shape {shape}, got {a.shape}")
+                arrs.append(a)
+            return to_model_dtype(np.stack(arrs), src.dtype)
+
+        def one(key, shape, required=True):
+            if key not in t:
+                if required:
+                    raise WeightKey(3, f"missing tensor {key}")
+                return None
+            a = np.asarray(t[key], np.float32)
+            if a.shape != shape:
+                raise WeightKey(3, f"{key}: expected shape {shape}, got {a.shape}")
+            return to_model_dtype(a, src.dtype)
+
+        D, H = int(dim), int(hidden)
+        ex = path + ".experts.{e}"
+        keep = [
+            one(f"{path}.router.weight", (E, D)),
+            stack(ex + ".gate.weight", (H, D), False), stack(ex + ".gate.bias", (H,), True),
+            stack(ex + ".up.weight", (H, D), False), stack(ex + ".up.bias", (H,), True),
+            stack(ex + ".down.weight", (D, H), False), stack(ex + ".down.bias", (D,), True),
+        ]
+        if cfg.shared_dense > 0:
+            dp = path + ".dense"
+            keep += [one(dp + ".gate.weight", (H, D)), one(dp + ".gate.bias", (H,), False),
+                     one(dp + ".up.weight", (H, D)), one(dp + ".up.bias", (H,), False),
+                     one(dp + ".down.weight", (D, H)), one(dp + ".down.bias", (D,), False)]
+        else:
+            keep += [None] * 6
+        ptrs = [None if a is None else a.ctypes.data for a in keep]
+        return _lib.lib().nomas_moe_from_host(C.byref(c), D, H, int(src.dtype), src.device,
+                                              *ptrs, C.byref(h))
+
+    # -- MoeLayer::forward (moe.rs:65-109) -----------------------------------
+    def forward(self, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        """x: (..., D) in the model dtype, on the layer's GPU or on the host."""
+        if x.dim() < 1 or x.shape[-1] != self.dim:
+            raise NomasError(2, f"expected last dim {self.dim}, got shape {tuple(x.shape)}")
+        if x.dtype != self.dtype.torch:
+            raise NomasError(2, f"expected dtype {self.dtype.torch}, got {x.dtype}")
+        xc = x.contiguous()
+        rows = xc.numel() // self.dim
+        if out is None:
+            out = torch.empty_like(xc)
+        L = _lib.lib()
+        if xc.is_cuda:
+            stream = torch.cuda.current_stream(xc.device).cuda_stream
+            _check(L.nomas_moe_forward(self._h, xc.data_ptr(), out.data_ptr(), rows, stream))
+        else:
+            _check(L.nomas_moe_forward_host(self._h, xc.data_ptr(), out.data_ptr(), rows))
+        return out
+
+    __call__ = forward
+
+    def n_params(self) -> int:
+        """moe.rs:112-114."""
+        return int(_lib.lib().nomas_moe_n_params(self._h))
+
+    def routing(self, rows: int):
+        """Routing of the last forward: (idx[rows,k] ascending, w[rows,k], counts[E], gap[rows])."""
+        k, E = self.top_k, self.experts
+        idx = np.empty((rows, k), np.int32)
+        w = np.empty((rows, k), np.float32)
+        counts = np.empty(E, np.int32)
+        gap = np.empty(rows, np.float32)
+        _check(_lib.lib().nomas_moe_routing(self._h, idx.ctypes.data, w.ctypes.data,
+                                            counts.ctypes.data, gap.ctypes.data))
+        return idx, w, counts, gap
+
+    def set_profiling(self, on: bool) -> None:
+        _check(_lib.lib().nomas_moe_set_profiling(self._h, 1 if on else 0))
+
+    STAGES = ("router", "scan", "dispatch", "gemm_gate_up", "gemm_down", "combine")
+
+    def stage_times(self) -> dict:
+        """Average per-stage milliseconds of the forwards profiled since the last call."""
+        ms = (C.c_float * 6)()
+        _check(_lib.lib().nomas_moe_stage_times(self._h, ms))
+        return dict(zip(self.STAGES, [float(v) for v in ms]))
+
+    @property
+    def uses_mfma(self) -> bool:
+        return bool(_lib.lib().nomas_moe_uses_mfma(self._h))
+
+    def close(self) -> None:
+        if self._h:
+            _lib.lib().nomas_moe_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

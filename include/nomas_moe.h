@@ -1,0 +1,148 @@
+/*
+ * nomas_moe.h -- C ABI of the MI355X (gfx950) top-k MoE feed-forward block.
+ *
+ * Drop-in for hy-nomas-rs `MoeLayer` (nomas-core/src/modules/moe.rs).  Every
+ * entry point below names the reference interface it replaces.  Plain
+ * pointers and sizes only; a Rust `extern "C"` block binds it 1:1.
+ *
+ * Conventions
+ *  - Every function returning `int` returns NOMAS_OK (0) or a NOMAS_ERR_* code;
+ *    the message of the last failure on the calling thread is available from
+ *    nomas_moe_last_error().  These map onto the reference's error variants
+ *    (nomas-core/src/error.rs:7-46): INVALID_CONFIG -> Error::InvalidConfig,
+ *    WEIGHT_KEY -> Error::WeightKey, IO -> Error::Io, everything else ->
+ *    Error::Candle / Error::Msg.
+ *  - Tensors are row-major.  A forward input of any rank >= 2 with last dim D
+ *    is passed as `rows` = product of the leading dims, exactly as Lin::fwd
+ *    folds leading dims (nomas-core/src/modules/mod.rs:132-134).
+ *  - Weights use the reference's (out, in) layout with experts concatenated:
+ *    router (E, D); gate/up (E, H, D) + bias (E, H); down (E, D, H) + bias (E, D).
+ *  - dtype codes follow nomas-core/src/config.rs:30-39 (DataType).
+ *  - A handle owns its device weights and workspace.  Calls on one handle
+ *    are not re-entrant: use one handle per concurrent stream.
+ */
+#ifndef NOMAS_MOE_H
+#define NOMAS_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum nomas_status {
+    NOMAS_OK = 0,
+    NOMAS_ERR_INVALID_CONFIG = 1,   /* config.rs:394-399 / shapes unsupported      */
+    NOMAS_ERR_INVALID_ARGUMENT = 2, /* null or misaligned pointer, bad row count   */
+    NOMAS_ERR_WEIGHT_KEY = 3,       /* weights.rs:117-127 missing / misshaped key  */
+    NOMAS_ERR_IO = 4,               /* checkpoint file could not be read           */
+    NOMAS_ERR_HIP = 5,              /* a HIP runtime call failed                   */
+    NOMAS_ERR_OUT_OF_MEMORY = 6,    /* device or host allocation failed            */
+    NOMAS_ERR_STATE = 7             /* e.g. routing read back before any forward   */
+};
+
+/* DataType (config.rs:30-39). */
+enum nomas_dtype { NOMAS_F32 = 0, NOMAS_BF16 = 1, NOMAS_F16 = 2 };
+
+/* MoeConfig (config.rs:202-213), field for field. */
+typedef struct nomas_moe_config {
+    int64_t experts;     /* number of experts                                   */
+    int64_t top_k;       /* experts activated per token                         */
+    double shared_dense; /* coefficient of the additive shared dense FFN (moe.rs:103-106) */
+    uint64_t seed;       /* carried for parity; unused, as in the reference     */
+} nomas_moe_config;
+
+typedef struct nomas_moe nomas_moe_t;
+
+/* NomasConfig::validate's MoE clause (config.rs:394-399): 1 <= top_k <= experts. */
+int nomas_moe_config_validate(const nomas_moe_config *cfg);
+
+/* MoeLayer::from_source with Weights::Random (moe.rs:26-62, mod.rs:38-45,80-95):
+ * router and experts drawn by xavier(path_seed(seed, "{path}.router" /
+ * "{path}.experts.{e}.{gate,up,down}" / "{path}.dense.*")), zero biases,
+ * rounded to `dtype`.  `device` is the HIP device ordinal. */
+int nomas_moe_from_random(const nomas_moe_config *cfg, const char *path, int64_t dim,
+                          int64_t hidden, int dtype, uint64_t seed, int device,
+                          nomas_moe_t **out);
+
+/* MoeLayer::from_source with Weights::Loaded (moe.rs:26-62, mod.rs:69-77,
+ * weights.rs:105-145): reads `{path}.router.weight`,
+ * `{path}.experts.{e}.{gate,up,down}.{weight,bias}` and, when shared_dense > 0,
+ * `{path}.dense.*` from the given safetensors files (later files override
+ * earlier ones), casting every tensor to `dtype` (weights.rs:129-133). */
+int nomas_moe_from_safetensors(const nomas_moe_config *cfg, const char *const *files,
+                               int64_t n_files, const char *path, int64_t dim, int64_t hidden,
+                               int dtype, int device, nomas_moe_t **out);
+
+/* MoeLayer from host arrays already in `dtype` (the tensors a VarBuilder would
+ * hand to Lin::load, mod.rs:69-77).  Bias pointers may be NULL (zero bias);
+ * the dense_* group is read only when cfg->shared_dense > 0. */
+int nomas_moe_from_host(const nomas_moe_config *cfg, int64_t dim, int64_t hidden, int dtype,
+                        int device, const void *router_w,
+                        const void *gate_w, const void *gate_b,
+                        const void *up_w, const void *up_b,
+                        const void *down_w, const void *down_b,
+                        const void *dense_gate_w, const void *dense_gate_b,
+                        const void *dense_up_w, const void *dense_up_b,
+                        const void *dense_down_w, const void *dense_down_b,
+                        nomas_moe_t **out);
+
+/* MoeLayer::forward (moe.rs:65-109) on device-resident tensors: x and y are
+ * (rows, D) in the handle's dtype, 16-byte aligned; `stream` is a
+ * hipStream_t (NULL = default stream).  Asynchronous with respect to the host. */
+int nomas_moe_forward(nomas_moe_t *h, const void *x, void *y, int64_t rows, void *stream);
+
+/* MoeLayer::forward on host tensors (the candle CPU-tensor case): copies x in,
+ * runs the forward, copies y out and synchronises. */
+int nomas_moe_forward_host(nomas_moe_t *h, const void *x, void *y, int64_t rows);
+
+/* MoeLayer::n_params (moe.rs:112-114): router + experts, dense excluded. */
+int64_t nomas_moe_n_params(const nomas_moe_t *h);
+
+/* Routing of the last forward, read back to host (no reference counterpart:
+ * the reference keeps it inside forward, moe.rs:92-95).  idx/w are rows x k
+ * with experts in ascending index order, counts has E entries, gap has one
+ * entry per row: logit of the k-th selected expert minus the best unselected
+ * one (+inf when k == E).  Any pointer may be NULL.  Synchronises. */
+int nomas_moe_routing(nomas_moe_t *h, int32_t *idx, float *w, int32_t *counts, float *gap);
+
+/* Dimensions of a handle: dim, hidden, experts, top_k, dtype (any may be NULL). */
+int nomas_moe_dims(const nomas_moe_t *h, int64_t *dim, int64_t *hidden, int64_t *experts,
+                   int64_t *top_k, int *dtype);
+
+/* Per-stage timing (no reference counterpart; measurement only).  When enabled,
+ * each forward records HIP events around its six stages on its stream;
+ * nomas_moe_stage_times returns the last forward's durations in milliseconds:
+ * [router, scan, dispatch, gemm_gate_up, gemm_down, combine].  Synchronises. */
+int nomas_moe_set_profiling(nomas_moe_t *h, int enable);
+int nomas_moe_stage_times(nomas_moe_t *h, float *ms6);
+
+/* Which GEMM path the handle uses: 1 = bf16/f16 MFMA grouped GEMM,
+ * 0 = general (any shape / f32) path. */
+int nomas_moe_uses_mfma(const nomas_moe_t *h);
+
+void nomas_moe_destroy(nomas_moe_t *h);
+
+/* Message of the last failure on this thread ("" if none). */
+const char *nomas_moe_last_error(void);
+
+/* Weights::path_seed (mod.rs:47-55): FNV-1a of `path` with the offset basis
+ * xor'ed with `seed`. */
+uint64_t nomas_path_seed(uint64_t seed, const char *path);
+
+/* deterministic_randn_affine (tensor_utils.rs:123-138): n f32 values of the
+ * SplitMix64 + Box-Muller stream `seed`, scaled by std and shifted by mean.
+ * Bit-identical to the reference; runs on host threads. */
+void nomas_randn_affine(uint64_t seed, double mean, double std, int64_t n, float *out);
+
+/* Host conversion helpers: f32 -> bf16 / f16 bit patterns, round to nearest
+ * even (candle's to_dtype, weights.rs:129-133). */
+void nomas_f32_to_bf16(const float *in, uint16_t *out, int64_t n);
+void nomas_f32_to_f16(const float *in, uint16_t *out, int64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NOMAS_MOE_H */

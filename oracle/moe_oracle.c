@@ -1,0 +1,483 @@
+/*
+ * moe_oracle.c -- CPU restatement of hy-nomas-rs `MoeLayer::forward` and of the
+ * deterministic generator its tests and random weights use.
+ *
+ * TEST INFRASTRUCTURE ONLY. This file is the checker, never the product: only
+ * the tests, the smoke check and the CPU-baseline leg of the benchmark load it.
+ * The product library never links or calls it.
+ *
+ * Reference files restated (paths relative to the reference repository):
+ *   nomas-core/src/tensor_utils.rs:65-106   SplitMix64 + Box-Muller
+ *   nomas-core/src/tensor_utils.rs:123-155  deterministic_randn_affine / uniform
+ *   nomas-core/src/tensor_utils.rs:159-162  xavier
+ *   nomas-core/src/modules/mod.rs:47-55     Weights::path_seed (FNV-1a)
+ *   nomas-core/src/modules/mod.rs:122-142   Lin::fwd  (x @ W^T + b, rows folded)
+ *   nomas-core/src/modules/moe.rs:65-109    MoeLayer::forward
+ *   nomas-core/src/modules/mlp.rs:42-46     FeedForward::SwiGlu
+ *
+ * Two evaluation modes:
+ *   - sparse f64  (orc_forward_sparse_f64): routing from f64 logits, only the
+ *     selected experts, f64 accumulation.  Used for parity at any size because
+ *     rows are independent, so any subset of rows can be checked exactly.
+ *   - faithful dense f32 (orc_forward_dense_f32): the reference algorithm as
+ *     written -- f32 routing composed as max/sub/exp/sum/div, iterative argmax,
+ *     every expert on every row, combine in ascending expert order.  This is
+ *     also the timed CPU baseline.
+ *
+ * Weight layout everywhere is the reference's (out, in), experts concatenated:
+ *   router wr (E, D); gate wg (E, H, D), bg (E, H); up wu (E, H, D), bu (E, H);
+ *   down wd (E, D, H), bd (E, D).  The optional shared dense branch uses the
+ *   same layout with E = 1 (moe.rs:44-54,103-106).
+ *
+ * `orc_mutation` plants one known mistake so the pin tests can prove they
+ * would catch it (0 = faithful).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+int orc_mutation = 0;
+
+enum {
+    MUT_NONE = 0,
+    MUT_BOXMULLER_SWAP = 1,   /* sin/cos order of the Box-Muller pair swapped   */
+    MUT_TIE_HIGH_INDEX = 2,   /* argmax ties resolved to the highest index      */
+    MUT_NO_RENORM = 3,        /* weights = raw softmax probs (no renormalise)   */
+    MUT_SWAP_GATE_UP = 4,     /* silu applied to the up projection              */
+    MUT_DROP_DOWN_BIAS = 5,   /* down-projection bias ignored                   */
+    MUT_DOWN_TRANSPOSED = 6,  /* down weight indexed (in, out) instead of (out, in) */
+    MUT_FNV_PRIME = 7,        /* FNV-1a with a wrong multiplier                 */
+    MUT_SPLITMIX_SHIFT = 8,   /* SplitMix64 first xor-shift 31 instead of 30    */
+    MUT_COMBINE_DESC = 9,     /* combine over experts in descending order (f32 only) */
+};
+
+/* ------------------------------------------------------------------ */
+/* Generator: tensor_utils.rs:65-106, mod.rs:47-55                     */
+/* ------------------------------------------------------------------ */
+
+/* SplitMix64::next_u64 (tensor_utils.rs:76-83). */
+uint64_t orc_splitmix64_next(uint64_t *state)
+{
+    *state += 0x9E3779B97F4A7C15ull;
+    uint64_t z = *state;
+    z = (z ^ (z >> (orc_mutation == MUT_SPLITMIX_SHIFT ? 31 : 30))) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+/* SplitMix64::next_f64 (tensor_utils.rs:86-89): 53 high bits scaled to [0, 1). */
+static double next_f64(uint64_t *state)
+{
+    return (double)(orc_splitmix64_next(state) >> 11) * (1.0 / 9007199254740992.0);
+}
+
+/* Weights::path_seed (mod.rs:47-55): FNV-1a over the path bytes, offset basis
+ * xor'ed with the base seed. */
+uint64_t orc_path_seed(uint64_t seed, const char *path)
+{
+    uint64_t h = 0xcbf29ce484222325ull ^ seed;
+    const uint64_t prime = orc_mutation == MUT_FNV_PRIME ? 0x100000001b5ull : 0x100000001b3ull;
+    for (const unsigned char *p = (const unsigned char *)path; *p; ++p) {
+        h ^= (uint64_t)*p;
+        h *= prime;
+    }
+    return h;
+}
+
+/* deterministic_randn_affine (tensor_utils.rs:123-138) with next_normal
+ * (tensor_utils.rs:93-106): each pair of draws (u1, u2) yields r*cos(theta)
+ * first and caches r*sin(theta) for the next element. */
+void orc_randn_affine(uint64_t seed, double mean, double std, int64_t n, float *out)
+{
+    uint64_t st = seed;
+    for (int64_t i = 0; i < n; i += 2) {
+        double u1 = next_f64(&st);
+        if (u1 < 2.2250738585072014e-308) /* f64::MIN_POSITIVE */
+            u1 = 2.2250738585072014e-308;
+        double u2 = next_f64(&st);
+        double r = sqrt(-2.0 * log(u1));
+        double theta = 2.0 * 3.14159265358979323846 * u2;
+        double a = r * cos(theta), b = r * sin(theta);
+        if (orc_mutation == MUT_BOXMULLER_SWAP) { double t = a; a = b; b = t; }
+        out[i] = (float)(a * std + mean);
+        if (i + 1 < n)
+            out[i + 1] = (float)(b * std + mean);
+    }
+}
+
+/* deterministic_uniform (tensor_utils.rs:141-155). */
+void orc_uniform(uint64_t seed, double lo, double hi, int64_t n, float *out)
+{
+    uint64_t st = seed;
+    for (int64_t i = 0; i < n; ++i)
+        out[i] = (float)(lo + next_f64(&st) * (hi - lo));
+}
+
+/* xavier (tensor_utils.rs:159-162): N(0, sqrt(2/(out+in))) of shape (out, in). */
+void orc_xavier(int64_t out_f, int64_t in_f, uint64_t seed, float *w)
+{
+    orc_randn_affine(seed, 0.0, sqrt(2.0 / (double)(out_f + in_f)), out_f * in_f, w);
+}
+
+/* f32 -> bf16 round-to-nearest-even, returned widened back to f32
+ * (candle's to_dtype(BF16) goes through half::bf16::from_f32, which is RNE). */
+void orc_round_bf16(float *a, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i) {
+        uint32_t u;
+        memcpy(&u, &a[i], 4);
+        if ((u & 0x7fffffffu) > 0x7f800000u) {
+            u = (u | 0x00400000u) & 0xffff0000u;
+        } else {
+            u += 0x7fffu + ((u >> 16) & 1u);
+            u &= 0xffff0000u;
+        }
+        memcpy(&a[i], &u, 4);
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* Routing: moe.rs:67-95                                               */
+/* ------------------------------------------------------------------ */
+
+/* Route one row in f64.  logits_e = sum_d x_d * wr[e][d] (ascending d),
+ * probs = softmax composed max/sub/exp/sum/div, top-k by k passes of argmax
+ * over the remaining probs (first maximum wins), weights = top / (sum + 1e-9).
+ * Writes the k selected experts in ascending index order with their weights,
+ * the E logits, and the logit gap between the k-th selected and the best
+ * unselected expert (+inf when k == E). */
+static void route_row_f64(int64_t D, int64_t E, int64_t k, const float *x, const float *wr,
+                          int32_t *idx, double *w, double *logits, double *gap, double *scratch)
+{
+    double *p = scratch;            /* E */
+    double *rem = scratch + E;      /* E */
+    double *top = scratch + 2 * E;  /* E */
+    for (int64_t e = 0; e < E; ++e) {
+        double s = 0.0;
+        const float *we = wr + e * D;
+        for (int64_t d = 0; d < D; ++d)
+            s += (double)x[d] * (double)we[d];
+        logits[e] = s;
+    }
+    double m = logits[0];
+    for (int64_t e = 1; e < E; ++e)
+        if (logits[e] > m) m = logits[e];
+    double sum = 0.0;
+    for (int64_t e = 0; e < E; ++e) {
+        p[e] = exp(logits[e] - m);
+        sum += p[e];
+    }
+    for (int64_t e = 0; e < E; ++e) {
+        p[e] /= sum;
+        rem[e] = p[e];
+        top[e] = 0.0;
+    }
+    for (int64_t it = 0; it < k; ++it) {
+        int64_t best = 0;
+        for (int64_t e = 1; e < E; ++e) {
+            if (orc_mutation == MUT_TIE_HIGH_INDEX ? rem[e] >= rem[best] : rem[e] > rem[best])
+                best = e;
+        }
+        top[best] += rem[best];
+        rem[best] = 0.0;
+    }
+    /* A selected expert is one whose remaining prob was zeroed; with no
+     * underflowed probabilities every selected entry of `top` is > 0. */
+    double norm = 0.0;
+    for (int64_t e = 0; e < E; ++e)
+        norm += top[e];
+    double kth = INFINITY, best_un = -INFINITY;
+    int64_t j = 0;
+    for (int64_t e = 0; e < E; ++e) {
+        if (top[e] > 0.0) {
+            if (j < k) {
+                idx[j] = (int32_t)e;
+                w[j] = orc_mutation == MUT_NO_RENORM ? top[e] : top[e] / (norm + 1e-9);
+            }
+            ++j;
+            if (logits[e] < kth) kth = logits[e];
+        } else if (logits[e] > best_un) {
+            best_un = logits[e];
+        }
+    }
+    for (; j < k; ++j) { idx[j] = -1; w[j] = 0.0; }
+    *gap = (k == E) ? INFINITY : kth - best_un;
+}
+
+/* Route T rows (x: T x D, wr: E x D).  Any output pointer may be NULL. */
+void orc_route_f64(int64_t T, int64_t D, int64_t E, int64_t k, const float *x, const float *wr,
+                   int32_t *idx, double *w, double *logits, double *gap)
+{
+#pragma omp parallel
+    {
+        double *scr = (double *)malloc(sizeof(double) * (size_t)(4 * E + 2 * k + 1));
+        int32_t *li = (int32_t *)malloc(sizeof(int32_t) * (size_t)k);
+#pragma omp for schedule(static)
+        for (int64_t t = 0; t < T; ++t) {
+            double *lg = scr + 3 * E, *lw = scr + 4 * E, g;
+            route_row_f64(D, E, k, x + t * D, wr, li, lw, lg, &g, scr);
+            if (idx) memcpy(idx + t * k, li, sizeof(int32_t) * (size_t)k);
+            if (w) memcpy(w + t * k, lw, sizeof(double) * (size_t)k);
+            if (logits) memcpy(logits + t * E, lg, sizeof(double) * (size_t)E);
+            if (gap) gap[t] = g;
+        }
+        free(scr);
+        free(li);
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* Sparse f64 forward of selected rows                                 */
+/* ------------------------------------------------------------------ */
+
+static double silu(double g) { return g / (1.0 + exp(-g)); }
+
+/* One SwiGLU FFN (mlp.rs:42-46) on one row, f64: y = down(silu(gate x) * up x). */
+static void swiglu_row_f64(int64_t D, int64_t H, const float *x, const float *wg, const float *bg,
+                           const float *wu, const float *bu, const float *wd, const float *bd,
+                           double *a, double *y)
+{
+    for (int64_t h = 0; h < H; ++h) {
+        double g = bg ? (double)bg[h] : 0.0, u = bu ? (double)bu[h] : 0.0;
+        const float *gr = wg + h * D, *ur = wu + h * D;
+        for (int64_t d = 0; d < D; ++d) {
+            g += (double)x[d] * (double)gr[d];
+            u += (double)x[d] * (double)ur[d];
+        }
+        if (orc_mutation == MUT_SWAP_GATE_UP) { double t = g; g = u; u = t; }
+        a[h] = silu(g) * u;
+    }
+    for (int64_t d = 0; d < D; ++d) {
+        double s = (bd && orc_mutation != MUT_DROP_DOWN_BIAS) ? (double)bd[d] : 0.0;
+        if (orc_mutation == MUT_DOWN_TRANSPOSED) {
+            /* reads wd as if it were laid out (in, out) = (H, D) */
+            for (int64_t h = 0; h < H; ++h)
+                s += a[h] * (double)wd[h * D + d];
+        } else {
+            const float *dr = wd + d * H;
+            for (int64_t h = 0; h < H; ++h)
+                s += a[h] * (double)dr[h];
+        }
+        y[d] = s;
+    }
+}
+
+/* out[r] = MoeLayer::forward(x)[rows[r]] for the listed rows, in f64.
+ * `rows` may be NULL to mean rows 0..nrows-1.  The shared dense branch
+ * (dense_* pointers, coefficient s) is added after the experts when s > 0,
+ * additively as moe.rs:103-106 does.  Also writes each row's routing when
+ * idx/w/gap are non-NULL (k entries per row, ascending expert index). */
+void orc_forward_sparse_f64(int64_t D, int64_t E, int64_t k, int64_t H,
+                            const float *x, const float *wr,
+                            const float *wg, const float *bg, const float *wu, const float *bu,
+                            const float *wd, const float *bd,
+                            double s, const float *dwg, const float *dbg, const float *dwu,
+                            const float *dbu, const float *dwd, const float *dbd,
+                            const int64_t *rows, int64_t nrows, double *out,
+                            int32_t *idx_out, double *w_out, double *gap_out)
+{
+#pragma omp parallel
+    {
+        double *scr = (double *)malloc(sizeof(double) * (size_t)(4 * E + 2 * k + H + D + 1));
+        int32_t *li = (int32_t *)malloc(sizeof(int32_t) * (size_t)k);
+#pragma omp for schedule(dynamic, 1)
+        for (int64_t r = 0; r < nrows; ++r) {
+            int64_t t = rows ? rows[r] : r;
+            const float *xr = x + t * D;
+            double *lg = scr + 3 * E, *lw = scr + 4 * E, *a = lw + k, *y = a + H, g;
+            route_row_f64(D, E, k, xr, wr, li, lw, lg, &g, scr);
+            double *o = out + r * D;
+            for (int64_t d = 0; d < D; ++d) o[d] = 0.0;
+            for (int64_t j = 0; j < k; ++j) {
+                int64_t e = li[j];
+                if (e < 0) continue;
+                swiglu_row_f64(D, H, xr, wg + e * H * D, bg ? bg + e * H : NULL,
+                               wu + e * H * D, bu ? bu + e * H : NULL,
+                               wd + e * D * H, bd ? bd + e * D : NULL, a, y);
+                for (int64_t d = 0; d < D; ++d) o[d] += lw[j] * y[d];
+            }
+            if (s > 0.0 && dwg) {
+                swiglu_row_f64(D, H, xr, dwg, dbg, dwu, dbu, dwd, dbd, a, y);
+                for (int64_t d = 0; d < D; ++d) o[d] += s * y[d];
+            }
+            if (idx_out) memcpy(idx_out + r * k, li, sizeof(int32_t) * (size_t)k);
+            if (w_out) memcpy(w_out + r * k, lw, sizeof(double) * (size_t)k);
+            if (gap_out) gap_out[r] = g;
+        }
+        free(scr);
+        free(li);
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* Faithful dense f32 forward (the reference algorithm; CPU baseline)   */
+/* ------------------------------------------------------------------ */
+
+typedef float v16f __attribute__((vector_size(64)));
+
+/* C (M x N, row-major, ldc) = A (M x K) . B (N x K)^T, both K-contiguous, as
+ * Lin::fwd's x.matmul(W^T) (mod.rs:135).  Cache-blocked with a 4x4 register
+ * tile of 16-wide dot-product accumulators; OpenMP over row/column blocks. */
+static void sgemm_nt(int64_t M, int64_t N, int64_t K, const float *A, const float *B, float *C,
+                     int64_t ldc)
+{
+    const int64_t MB = 64, NB = 64;
+    int64_t mblocks = (M + MB - 1) / MB, nblocks = (N + NB - 1) / NB;
+    int64_t K16 = K & ~(int64_t)15;
+#pragma omp parallel for collapse(2) schedule(dynamic, 1)
+    for (int64_t mb = 0; mb < mblocks; ++mb) {
+        for (int64_t nb = 0; nb < nblocks; ++nb) {
+            int64_t m1 = mb * MB + MB < M ? mb * MB + MB : M;
+            int64_t n1 = nb * NB + NB < N ? nb * NB + NB : N;
+            for (int64_t m = mb * MB; m < m1; m += 4) {
+                for (int64_t n = nb * NB; n < n1; n += 4) {
+                    int64_t mr = m1 - m < 4 ? m1 - m : 4, nr = n1 - n < 4 ? n1 - n : 4;
+                    v16f acc[4][4];
+                    memset(acc, 0, sizeof(acc));
+                    const float *ap[4], *bp[4];
+                    for (int i = 0; i < 4; ++i) ap[i] = A + (m + (i < mr ? i : 0)) * K;
+                    for (int j = 0; j < 4; ++j) bp[j] = B + (n + (j < nr ? j : 0)) * K;
+                    for (int64_t kk = 0; kk < K16; kk += 16) {
+                        v16f av[4], bv[4];
+                        for (int i = 0; i < 4; ++i) memcpy(&av[i], ap[i] + kk, 64);
+                        for (int j = 0; j < 4; ++j) memcpy(&bv[j], bp[j] + kk, 64);
+                        for (int i = 0; i < 4; ++i)
+                            for (int j = 0; j < 4; ++j)
+                                acc[i][j] += av[i] * bv[j];
+                    }
+                    for (int i = 0; i < mr; ++i) {
+                        for (int j = 0; j < nr; ++j) {
+                            float s = 0.0f;
+                            for (int l = 0; l < 16; ++l) s += acc[i][j][l];
+                            for (int64_t kk = K16; kk < K; ++kk) s += ap[i][kk] * bp[j][kk];
+                            C[(m + i) * ldc + n + j] = s;
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+/* SwiGLU on all T rows in f32 (mlp.rs:42-46 via Lin::fwd, mod.rs:122-142):
+ * each op rounded to f32 as candle does. G and U are T x H scratch. */
+static void swiglu_dense_f32(int64_t T, int64_t D, int64_t H, const float *x, const float *wg,
+                             const float *bg, const float *wu, const float *bu, const float *wd,
+                             const float *bd, float *G, float *U, float *Y)
+{
+    sgemm_nt(T, H, D, x, wg, G, H);
+    sgemm_nt(T, H, D, x, wu, U, H);
+#pragma omp parallel for schedule(static)
+    for (int64_t t = 0; t < T; ++t) {
+        for (int64_t h = 0; h < H; ++h) {
+            float g = G[t * H + h] + (bg ? bg[h] : 0.0f);
+            float u = U[t * H + h] + (bu ? bu[h] : 0.0f);
+            float sg = g / (1.0f + expf(-g));
+            G[t * H + h] = sg * u;
+        }
+    }
+    sgemm_nt(T, D, H, G, wd, Y, D);
+    if (bd) {
+#pragma omp parallel for schedule(static)
+        for (int64_t t = 0; t < T; ++t)
+            for (int64_t d = 0; d < D; ++d) Y[t * D + d] += bd[d];
+    }
+}
+
+/* The reference MoeLayer::forward (moe.rs:65-109) in f32, every expert on
+ * every row.  Routing: f32 logits, softmax max/sub/exp/sum/div, k passes of
+ * argmax (first max wins) with the selected entry zeroed, weights
+ * top / (sum_E top + 1e-9).  Combine: out = out + y_e * w_e in ascending e,
+ * then out + s * dense(x).  Writes the dense (T x E) weights when w_dense is
+ * non-NULL.  Scratch is allocated internally (3 * T * max(H, D) floats). */
+int orc_forward_dense_f32(int64_t T, int64_t D, int64_t E, int64_t k, int64_t H,
+                          const float *x, const float *wr,
+                          const float *wg, const float *bg, const float *wu, const float *bu,
+                          const float *wd, const float *bd,
+                          double s, const float *dwg, const float *dbg, const float *dwu,
+                          const float *dbu, const float *dwd, const float *dbd,
+                          float *out, float *w_dense)
+{
+    int64_t HD = H > D ? H : D;
+    float *logits = (float *)malloc(sizeof(float) * (size_t)(T * E));
+    float *wts = (float *)malloc(sizeof(float) * (size_t)(T * E));
+    float *G = (float *)malloc(sizeof(float) * (size_t)(T * HD));
+    float *U = (float *)malloc(sizeof(float) * (size_t)(T * HD));
+    float *Y = (float *)malloc(sizeof(float) * (size_t)(T * D));
+    if (!logits || !wts || !G || !U || !Y) {
+        free(logits); free(wts); free(G); free(U); free(Y);
+        return -1;
+    }
+    sgemm_nt(T, E, D, x, wr, logits, E);
+#pragma omp parallel for schedule(static)
+    for (int64_t t = 0; t < T; ++t) {
+        float *l = logits + t * E, *w = wts + t * E;
+        float m = l[0];
+        for (int64_t e = 1; e < E; ++e) if (l[e] > m) m = l[e];
+        float sum = 0.0f;
+        for (int64_t e = 0; e < E; ++e) { w[e] = expf(l[e] - m); sum += w[e]; }
+        for (int64_t e = 0; e < E; ++e) w[e] = w[e] / sum;  /* w holds probs = remaining */
+        float top[1024];
+        float *tp = E <= 1024 ? top : (float *)malloc(sizeof(float) * (size_t)E);
+        for (int64_t e = 0; e < E; ++e) tp[e] = 0.0f;
+        for (int64_t it = 0; it < k; ++it) {
+            int64_t best = 0;
+            for (int64_t e = 1; e < E; ++e)
+                if (orc_mutation == MUT_TIE_HIGH_INDEX ? w[e] >= w[best] : w[e] > w[best]) best = e;
+            float sel = w[best];
+            tp[best] = tp[best] + sel;
+            w[best] = w[best] - sel;
+        }
+        float norm = 0.0f;
+        for (int64_t e = 0; e < E; ++e) norm += tp[e];
+        for (int64_t e = 0; e < E; ++e)
+            w[e] = orc_mutation == MUT_NO_RENORM ? tp[e] : tp[e] / (norm + 1e-9f);
+        if (tp != top) free(tp);
+    }
+    if (w_dense) memcpy(w_dense, wts, sizeof(float) * (size_t)(T * E));
+    memset(out, 0, sizeof(float) * (size_t)(T * D));
+    for (int64_t ei = 0; ei < E; ++ei) {
+        int64_t e = orc_mutation == MUT_COMBINE_DESC ? E - 1 - ei : ei;
+        swiglu_dense_f32(T, D, H, x, wg + e * H * D, bg ? bg + e * H : NULL, wu + e * H * D,
+                         bu ? bu + e * H : NULL, wd + e * D * H, bd ? bd + e * D : NULL, G, U, Y);
+#pragma omp parallel for schedule(static)
+        for (int64_t t = 0; t < T; ++t) {
+            float we = wts[t * E + e];
+            for (int64_t d = 0; d < D; ++d) {
+                float prod = Y[t * D + d] * we;
+                out[t * D + d] = out[t * D + d] + prod;
+            }
+        }
+    }
+    if (s > 0.0 && dwg) {
+        swiglu_dense_f32(T, D, H, x, dwg, dbg, dwu, dbu, dwd, dbd, G, U, Y);
+        float sf = (float)s;
+#pragma omp parallel for schedule(static)
+        for (int64_t t = 0; t < T; ++t)
+            for (int64_t d = 0; d < D; ++d) out[t * D + d] = out[t * D + d] + Y[t * D + d] * sf;
+    }
+    free(logits); free(wts); free(G); free(U); free(Y);
+    return 0;
+}
+
+int orc_num_threads(void)
+{
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+void orc_set_num_threads(int n)
+{
+#ifdef _OPENMP
+    if (n > 0) omp_set_num_threads(n);
+#else
+    (void)n;
+#endif
+}
