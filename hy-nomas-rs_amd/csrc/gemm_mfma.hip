@@ -76,12 +76,17 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
     using V = typename Mfma<T>::V;
     constexpr int WM = BM / 2, WN = BN / 2;       // wave tile: token rows x weight rows
     constexpr int SM = WM / 32, SN = WN / 32;     // 32x32 MFMA blocks per wave
-    constexpr int LW = BN * 8 / kThreads;         // 16-byte chunks per thread per k step
-    constexpr int LX = BM * 8 / kThreads;
+    // Direct global->LDS loads: one wave instruction fills 8 rows x 128 bytes.
+    constexpr int QW = BN / 8 / (kThreads / kWave);  // load instructions per wave per k step
+    constexpr int QX = BM / 8 / (kThreads / kWave);
     static_assert(MODE == kDown || SN % 2 == 0, "gate/up pairs need an even block count");
 
-    __shared__ __attribute__((aligned(16))) T sW[2][BN * kBK];
-    __shared__ __attribute__((aligned(16))) T sX[2][BM * kBK];
+    // Two stages, each its own LDS object so the compiler can tell a stage
+    // being filled from the one being read.
+    __shared__ __attribute__((aligned(16))) T sW0[BN * kBK];
+    __shared__ __attribute__((aligned(16))) T sX0[BM * kBK];
+    __shared__ __attribute__((aligned(16))) T sW1[BN * kBK];
+    __shared__ __attribute__((aligned(16))) T sX1[BM * kBK];
 
     const int N = a.N, K = a.K;
     int mt, nt;
@@ -99,22 +104,21 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
     const T* Wt = static_cast<const T*>(a.W) + ((int64_t)e * N + n0) * K;
     const T* Xt = static_cast<const T*>(a.X) + (int64_t)row0 * K;
 
-    const int lc = tid & 7, lr = tid >> 3;
-    int woff[LW], xoff[LX], wlds[LW], xlds[LX];
+    // Lane l of load instruction q writes LDS bytes [q*1024 + l*16, +16): tile
+    // row r = 8q + l/8, stored chunk l%8, which holds logical chunk
+    // (l%8) ^ swz(r) of that row -- the swizzle is applied on the global side.
+    int woff[QW], xoff[QX];
 #pragma unroll
-    for (int i = 0; i < LW; ++i) {
-        const int r = lr + 32 * i;
-        woff[i] = r * K + lc * 8;
-        wlds[i] = r * kBK + ((lc ^ swz(r)) * 8);
+    for (int i = 0; i < QW; ++i) {
+        const int r = (wave * QW + i) * 8 + (lane >> 3);
+        woff[i] = r * K + (((lane & 7) ^ swz(r)) * 8);
     }
 #pragma unroll
-    for (int i = 0; i < LX; ++i) {
-        const int r = lr + 32 * i;
+    for (int i = 0; i < QX; ++i) {
+        const int r = (wave * QX + i) * 8 + (lane >> 3);
         const int rr = r < nrows ? r : nrows - 1;
-        xoff[i] = rr * K + lc * 8;
-        xlds[i] = r * kBK + ((lc ^ swz(r)) * 8);
+        xoff[i] = rr * K + (((lane & 7) ^ swz(r)) * 8);
     }
-    uint4 rw[LW], rx[LX];
 
     f32x16_t acc[SN][SM];
 #pragma unroll
@@ -124,28 +128,24 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    auto gload = [&](int kt) {
+    auto issue = [&](int kt, T* dW, T* dX) {
         const int ko = kt * kBK;
 #pragma unroll
-        for (int i = 0; i < LW; ++i) rw[i] = *reinterpret_cast<const uint4*>(Wt + woff[i] + ko);
+        for (int i = 0; i < QW; ++i)
+            __builtin_amdgcn_global_load_lds(
+                (const void*)(Wt + woff[i] + ko),
+                (__attribute__((address_space(3))) void*)(dW + (wave * QW + i) * 8 * kBK), 16, 0, 0);
 #pragma unroll
-        for (int i = 0; i < LX; ++i) rx[i] = *reinterpret_cast<const uint4*>(Xt + xoff[i] + ko);
+        for (int i = 0; i < QX; ++i)
+            __builtin_amdgcn_global_load_lds(
+                (const void*)(Xt + xoff[i] + ko),
+                (__attribute__((address_space(3))) void*)(dX + (wave * QX + i) * 8 * kBK), 16, 0, 0);
+        // keep the loads ahead of the MFMAs that follow (the scheduler would
+        // otherwise sink them to the wait at the end of the stage)
+        __builtin_amdgcn_sched_barrier(0);
     };
-    auto lstore = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < LW; ++i) *reinterpret_cast<uint4*>(&sW[buf][wlds[i]]) = rw[i];
-#pragma unroll
-        for (int i = 0; i < LX; ++i) *reinterpret_cast<uint4*>(&sX[buf][xlds[i]]) = rx[i];
-    };
-
-    const int KT = K / kBK;
-    gload(0);
-    lstore(0);
-    __syncthreads();
     const int l32 = lane & 31, lhi = lane >> 5;
-    for (int kt = 0; kt < KT; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < KT) gload(kt + 1);
+    auto compute = [&](const T* cW, const T* cX) {
 #pragma unroll
         for (int ks = 0; ks < kBK / 16; ++ks) {
             const int kc = ks * 2 + lhi;
@@ -153,21 +153,38 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
 #pragma unroll
             for (int i = 0; i < SN; ++i) {
                 const int r = wn * WN + i * 32 + l32;
-                av[i] = *reinterpret_cast<const V*>(&sW[cur][r * kBK + ((kc ^ swz(r)) * 8)]);
+                av[i] = *reinterpret_cast<const V*>(&cW[r * kBK + ((kc ^ swz(r)) * 8)]);
             }
 #pragma unroll
             for (int j = 0; j < SM; ++j) {
                 const int r = wm * WM + j * 32 + l32;
-                bv[j] = *reinterpret_cast<const V*>(&sX[cur][r * kBK + ((kc ^ swz(r)) * 8)]);
+                bv[j] = *reinterpret_cast<const V*>(&cX[r * kBK + ((kc ^ swz(r)) * 8)]);
             }
 #pragma unroll
             for (int i = 0; i < SN; ++i)
 #pragma unroll
                 for (int j = 0; j < SM; ++j) acc[i][j] = Mfma<T>::run(av[i], bv[j], acc[i][j]);
         }
-        if (kt + 1 < KT) lstore(cur ^ 1);
+    };
+    // All of this wave's loads have landed, then every wave's have.
+    auto land = [&]() {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
+    };
+
+    const int KT = K / kBK;
+    issue(0, sW0, sX0);
+    land();
+    int kt = 0;
+    for (; kt + 2 <= KT; kt += 2) {
+        issue(kt + 1, sW1, sX1);
+        compute(sW0, sX0);
+        land();
+        if (kt + 2 < KT) issue(kt + 2, sW0, sX0);
+        compute(sW1, sX1);
+        land();
     }
+    if (kt < KT) compute(sW0, sX0);  // odd number of k steps: the last one is staged in 0
 
     // Epilogue.  Lane (l32, lhi) of block (i, j) holds token row
     // wm*WM + j*32 + l32 and weight rows wn*WN + i*32 + 8*(r/4) + 4*lhi + r%4.
