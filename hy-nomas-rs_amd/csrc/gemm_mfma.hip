@@ -11,19 +11,24 @@
 //    token rows the "B" operand, so each lane's accumulator holds 4
 //    consecutive output columns of one token row (8-byte stores).
 //  - v_mfma_f32_32x32x16_{bf16,f16}; 4 waves in a 2 x 2 grid, each wave a
-//    (BN/2) x (BM/2) tile of 32 x 32 MFMA blocks.
-//  - K is walked in 64-wide steps through double-buffered LDS tiles.  Rows of
-//    128 bytes are stored with their 16-byte chunks XOR-swizzled by
-//    (r ^ r >> 3) & 7, which keeps both the 16-byte row-chunk stores and the
-//    32-row MFMA operand reads free of bank conflicts.
+//    (BN/2) x (BM/2) tile of 32 x 32 MFMA blocks (256 f32 accumulators per
+//    lane for 256 x 256 tiles, held in AGPRs).
+//  - K is walked in BK-wide steps through a ring of S LDS stages filled by
+//    direct global->LDS loads (global_load_lds_dwordx4: no VGPR staging).
+//    Loads run S-1 steps ahead of the MFMAs; each step waits only for its own
+//    stage (partial vmcnt) and synchronises the block once.
+//  - LDS rows (BK * 2 bytes) keep their 16-byte chunks XOR-swizzled, so the
+//    32-row MFMA operand reads (ds_read_b128) are free of bank conflicts.  The
+//    swizzle is applied on the global side: lane l of a load instruction always
+//    writes LDS slot l, and reads the global chunk that belongs there.
 //  - Gate and up rows are interleaved in groups of 32 when the weights are
 //    packed (rows 64g..64g+31 = gate 32g.., rows 64g+32.. = up 32g..), so a
 //    wave holds gate and up of the same hidden unit in the same lane and the
 //    SwiGLU is applied in the epilogue without an extra pass over HBM.
-//  - Tiles are ordered in groups of GM row tiles (column index fastest within
-//    a group) and the grid is remapped so each XCD (block i runs on XCD i % 8)
-//    gets one contiguous range of that order: its concurrently running blocks
-//    share weight and token panels in the XCD's own L2.
+//  - Tiles are ordered in groups of kGroupM row tiles (column index fastest
+//    within a group) and the grid is remapped so each XCD (block i runs on XCD
+//    i % 8) gets one contiguous range of that order: its concurrently running
+//    blocks share weight and token panels in the XCD's own L2.
 #include "kernels.hpp"
 
 namespace nomas {
@@ -50,47 +55,99 @@ template <> struct Mfma<_Float16> {
 
 enum { kGateUp = 0, kDown = 1 };
 
-constexpr int kBK = 64;
 constexpr int kThreads = 256;
 constexpr int kGroupM = 4;
+constexpr int kBK = 32;     // k step
+#ifndef NOMAS_GEMM_STAGES
+#define NOMAS_GEMM_STAGES 4
+#endif
+constexpr int kStages = NOMAS_GEMM_STAGES;  // LDS ring depth
 
-__device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }
+// Physical 16-byte chunk of logical chunk c in LDS row r (CH chunks per row).
+template <int CH>
+__device__ __forceinline__ int swz(int r) {
+    if constexpr (CH == 8) return (r ^ (r >> 3)) & 7;
+    else return ((r >> 1) ^ (r >> 3)) & 3;
+}
 
-// Maps the hardware block id to (row tile, column tile).
-__device__ __forceinline__ void tile_coords(int pid, int G, int ntn, int max_tiles, int* mt,
-                                            int* nt) {
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Direct global->LDS load of 16 bytes per lane: lane l's bytes land at LDS
+// address lds_base + 16 * l (global_load_lds_dwordx4, M0 = LDS base; one wait
+// state between the M0 write and the load).  Issued as inline assembly so the
+// compiler does not track it: completion is waited for explicitly with
+// wait_vmcnt, and nothing else in these kernels uses M0.
+__device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(gptr), "s"(lds_base)
+                 : "memory", "m0");
+}
+
+template <typename P>
+__device__ __forceinline__ uint32_t lds_addr(P* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+// Maps the hardware block id to (row tile, column tile); returns false for
+// padding blocks.  Blocks are dispatched in id order, block i to XCD i % 8,
+// so one XCD's queue is ids x, x+8, ...  Its k-th group of kCusPerXcd
+// consecutive queue entries ("round") runs roughly at time k.  Round
+// R = k * 8 + x takes logical tiles [R * kCusPerXcd, (R + 1) * kCusPerXcd):
+// at any time the eight XCDs work on eight consecutive rounds (the same
+// expert's weights, shared through the MALL), and inside an XCD a round is a
+// kGroupM x 8 block of tiles sharing panels in that XCD's L2.  The grid is
+// padded to a multiple of 8 * kCusPerXcd.
+constexpr int kCusPerXcd = 32;
+__device__ __forceinline__ bool tile_coords(int pid, int ntn, int max_tiles, int* mt, int* nt) {
     const int xcd = pid % kNumXcd, loc = pid / kNumXcd;
-    const int per = (G + kNumXcd - 1) / kNumXcd;
-    const int tall = (G % kNumXcd) == 0 ? kNumXcd : G % kNumXcd;
-    const int L = xcd < tall ? xcd * per + loc : tall * per + (xcd - tall) * (per - 1) + loc;
+    const int round = (loc / kCusPerXcd) * kNumXcd + xcd;
+    const int L = round * kCusPerXcd + loc % kCusPerXcd;
     const int group = L / (kGroupM * ntn);
     const int first_m = group * kGroupM;
+    if (first_m >= max_tiles) return false;
     const int gm = min(kGroupM, max_tiles - first_m);
     const int within = L - group * kGroupM * ntn;
     *mt = first_m + within % gm;
     *nt = within / gm;
+    return true;
 }
 
-template <typename T, int MODE, int BM, int BN>
+template <typename T, int MODE, int BM, int BN, int BK, int S>
 __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
     using V = typename Mfma<T>::V;
     constexpr int WM = BM / 2, WN = BN / 2;       // wave tile: token rows x weight rows
     constexpr int SM = WM / 32, SN = WN / 32;     // 32x32 MFMA blocks per wave
-    // Direct global->LDS loads: one wave instruction fills 8 rows x 128 bytes.
-    constexpr int QW = BN / 8 / (kThreads / kWave);  // load instructions per wave per k step
-    constexpr int QX = BM / 8 / (kThreads / kWave);
+    constexpr int CH = BK / 8;                    // 16-byte chunks per LDS row
+    constexpr int RPI = kWave / CH;               // rows filled by one load instruction
+    constexpr int NW = kThreads / kWave;
+    constexpr int QW = BN / RPI / NW;             // load instructions per wave per k step
+    constexpr int QX = BM / RPI / NW;
+    constexpr int Q = QW + QX;
     static_assert(MODE == kDown || SN % 2 == 0, "gate/up pairs need an even block count");
+    static_assert(S >= 3 && S <= 5, "ring depth");
+    static_assert((S - 2) * Q <= 63, "vmcnt range");
 
-    // Two stages, each its own LDS object so the compiler can tell a stage
-    // being filled from the one being read.
-    __shared__ __attribute__((aligned(16))) T sW0[BN * kBK];
-    __shared__ __attribute__((aligned(16))) T sX0[BM * kBK];
-    __shared__ __attribute__((aligned(16))) T sW1[BN * kBK];
-    __shared__ __attribute__((aligned(16))) T sX1[BM * kBK];
+    // One LDS object per stage: the compiler then knows a stage being read is
+    // not the target of the loads in flight, and inserts no vmcnt(0) before
+    // the reads.  Stage indices are compile-time after unrolling.
+    __shared__ __attribute__((aligned(16))) T sW0[BN * BK], sW1[BN * BK], sW2[BN * BK],
+        sW3[S > 3 ? BN * BK : 8], sW4[S > 4 ? BN * BK : 8];
+    __shared__ __attribute__((aligned(16))) T sX0[BM * BK], sX1[BM * BK], sX2[BM * BK],
+        sX3[S > 3 ? BM * BK : 8], sX4[S > 4 ? BM * BK : 8];
+    auto stW = [&](int s) -> T* {
+        return s == 0 ? sW0 : s == 1 ? sW1 : s == 2 ? sW2 : s == 3 ? sW3 : sW4;
+    };
+    auto stX = [&](int s) -> T* {
+        return s == 0 ? sX0 : s == 1 ? sX1 : s == 2 ? sX2 : s == 3 ? sX3 : sX4;
+    };
 
     const int N = a.N, K = a.K;
     int mt, nt;
-    tile_coords(blockIdx.x, gridDim.x, N / BN, a.max_tiles, &mt, &nt);
+    if (!tile_coords(blockIdx.x, N / BN, a.max_tiles, &mt, &nt)) return;
     if (mt >= *a.tile_total) return;
     const TileInfo ti = a.tiles[mt];
     const int e = ti.expert, row0 = ti.row0, nrows = ti.rows;
@@ -105,19 +162,19 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
     const T* Xt = static_cast<const T*>(a.X) + (int64_t)row0 * K;
 
     // Lane l of load instruction q writes LDS bytes [q*1024 + l*16, +16): tile
-    // row r = 8q + l/8, stored chunk l%8, which holds logical chunk
-    // (l%8) ^ swz(r) of that row -- the swizzle is applied on the global side.
+    // row r = RPI*q + l/CH, stored chunk l%CH, which holds logical chunk
+    // (l%CH) ^ swz(r) of that row.
     int woff[QW], xoff[QX];
 #pragma unroll
     for (int i = 0; i < QW; ++i) {
-        const int r = (wave * QW + i) * 8 + (lane >> 3);
-        woff[i] = r * K + (((lane & 7) ^ swz(r)) * 8);
+        const int r = (wave * QW + i) * RPI + lane / CH;
+        woff[i] = r * K + (((lane % CH) ^ swz<CH>(r)) * 8);
     }
 #pragma unroll
     for (int i = 0; i < QX; ++i) {
-        const int r = (wave * QX + i) * 8 + (lane >> 3);
+        const int r = (wave * QX + i) * RPI + lane / CH;
         const int rr = r < nrows ? r : nrows - 1;
-        xoff[i] = rr * K + (((lane & 7) ^ swz(r)) * 8);
+        xoff[i] = rr * K + (((lane % CH) ^ swz<CH>(r)) * 8);
     }
 
     f32x16_t acc[SN][SM];
@@ -128,63 +185,87 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    auto issue = [&](int kt, T* dW, T* dX) {
-        const int ko = kt * kBK;
+    const int uwave = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform (SGPR) copy
+    auto issue = [&](int kt, int buf) {
+        const int ko = kt * BK;
+        const uint32_t bw = lds_addr(stW(buf)) + uwave * QW * RPI * BK * (int)sizeof(T);
+        const uint32_t bx = lds_addr(stX(buf)) + uwave * QX * RPI * BK * (int)sizeof(T);
 #pragma unroll
         for (int i = 0; i < QW; ++i)
-            __builtin_amdgcn_global_load_lds(
-                (const void*)(Wt + woff[i] + ko),
-                (__attribute__((address_space(3))) void*)(dW + (wave * QW + i) * 8 * kBK), 16, 0, 0);
+            lds_dma16(Wt + woff[i] + ko, bw + i * RPI * BK * (int)sizeof(T));
 #pragma unroll
         for (int i = 0; i < QX; ++i)
-            __builtin_amdgcn_global_load_lds(
-                (const void*)(Xt + xoff[i] + ko),
-                (__attribute__((address_space(3))) void*)(dX + (wave * QX + i) * 8 * kBK), 16, 0, 0);
-        // keep the loads ahead of the MFMAs that follow (the scheduler would
-        // otherwise sink them to the wait at the end of the stage)
+            lds_dma16(Xt + xoff[i] + ko, bx + i * RPI * BK * (int)sizeof(T));
+        // keep the loads ahead of the MFMAs that follow
         __builtin_amdgcn_sched_barrier(0);
     };
     const int l32 = lane & 31, lhi = lane >> 5;
-    auto compute = [&](const T* cW, const T* cX) {
+    // MFMAs of stage `buf`, with the Q loads of step `ktl` into stage `bufl`
+    // spread through them (one load per NMF / Q MFMAs): a burst of loads at
+    // the top of the stage would stall this wave's in-order issue while the
+    // memory pipeline drains, and with it the MFMAs behind them.
+    constexpr int NMF = (BK / 16) * SN * SM;
+    constexpr int EVERY = NMF / Q;
+    static_assert(NMF % Q == 0, "loads must divide the MFMA count");
+    auto compute_issue = [&](int buf, int ktl, int bufl) {
+        const T* cW = stW(buf);
+        const T* cX = stX(buf);
+        const int ko = ktl * BK;
+        const uint32_t bw = lds_addr(stW(bufl)) + uwave * QW * RPI * BK * (int)sizeof(T);
+        const uint32_t bx = lds_addr(stX(bufl)) + uwave * QX * RPI * BK * (int)sizeof(T);
 #pragma unroll
-        for (int ks = 0; ks < kBK / 16; ++ks) {
+        for (int ks = 0; ks < BK / 16; ++ks) {
             const int kc = ks * 2 + lhi;
             V av[SN], bv[SM];
 #pragma unroll
             for (int i = 0; i < SN; ++i) {
                 const int r = wn * WN + i * 32 + l32;
-                av[i] = *reinterpret_cast<const V*>(&cW[r * kBK + ((kc ^ swz(r)) * 8)]);
+                av[i] = *reinterpret_cast<const V*>(&cW[r * BK + ((kc ^ swz<CH>(r)) * 8)]);
             }
 #pragma unroll
             for (int j = 0; j < SM; ++j) {
                 const int r = wm * WM + j * 32 + l32;
-                bv[j] = *reinterpret_cast<const V*>(&cX[r * kBK + ((kc ^ swz(r)) * 8)]);
+                bv[j] = *reinterpret_cast<const V*>(&cX[r * BK + ((kc ^ swz<CH>(r)) * 8)]);
             }
 #pragma unroll
-            for (int i = 0; i < SN; ++i)
+            for (int i = 0; i < SN; ++i) {
 #pragma unroll
-                for (int j = 0; j < SM; ++j) acc[i][j] = Mfma<T>::run(av[i], bv[j], acc[i][j]);
+                for (int j = 0; j < SM; ++j) {
+                    const int m = (ks * SN + i) * SM + j;  // compile-time after unrolling
+                    if (m % EVERY == 0) {
+                        const int q = m / EVERY;
+                        if (q < QW) lds_dma16(Wt + woff[q] + ko, bw + q * RPI * BK * (int)sizeof(T));
+                        else lds_dma16(Xt + xoff[q - QW] + ko, bx + (q - QW) * RPI * BK * (int)sizeof(T));
+                    }
+                    acc[i][j] = Mfma<T>::run(av[i], bv[j], acc[i][j]);
+                }
+            }
         }
     };
-    // All of this wave's loads have landed, then every wave's have.
-    auto land = [&]() {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-    };
 
-    const int KT = K / kBK;
-    issue(0, sW0, sX0);
-    land();
-    int kt = 0;
-    for (; kt + 2 <= KT; kt += 2) {
-        issue(kt + 1, sW1, sX1);
-        compute(sW0, sX0);
-        land();
-        if (kt + 2 < KT) issue(kt + 2, sW0, sX0);
-        compute(sW1, sX1);
-        land();
+    // K / BK is a multiple of S (checked by the launcher).  Step kt computes
+    // stage kt % S.  Before it, the loads of stages <= kt must have landed:
+    // this wave's by vmcnt (exactly S - 2 later stages stay in flight), every
+    // wave's by the barrier.  The barrier also frees stage (kt - 1) % S, which
+    // is refilled with step kt + S - 1.  Past the end the last step is loaded
+    // again into that freed (never again read) stage, which keeps the loop
+    // free of branches and the in-flight count constant.  A bare s_barrier is
+    // used: __syncthreads() would add a full vmcnt(0) fence.
+    const int KT = K / BK;
+#pragma unroll
+    for (int s = 0; s < S - 1; ++s) issue(s, s);
+    for (int kt0 = 0; kt0 < KT; kt0 += S) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const int kt = kt0 + s;
+            wait_vmcnt<(S - 2) * Q>();
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            compute_issue(s, min(kt + S - 1, KT - 1), (s + S - 1) % S);
+        }
     }
-    if (kt < KT) compute(sW0, sX0);  // odd number of k steps: the last one is staged in 0
+    // drain the trailing loads before this block's LDS can be handed on
+    wait_vmcnt<0>();
 
     // Epilogue.  Lane (l32, lhi) of block (i, j) holds token row
     // wm*WM + j*32 + l32 and weight rows wn*WN + i*32 + 8*(r/4) + 4*lhi + r%4.
@@ -245,12 +326,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
 template <typename T, int MODE>
 hipError_t launch_mfma_t(const GemmArgs& a, hipStream_t s) {
     constexpr int BM = kMfmaBM, BN = kMfmaBN;
-    if (a.N % BN != 0 || a.K % kBK != 0) return hipErrorInvalidValue;
-    const int64_t grid = (int64_t)a.max_tiles * (a.N / BN);
+    if (a.N % BN != 0 || a.K % (kBK * kStages) != 0) return hipErrorInvalidValue;
+    constexpr int64_t pad = (int64_t)kNumXcd * kCusPerXcd;
+    const int64_t grid = ((int64_t)a.max_tiles * (a.N / BN) + pad - 1) / pad * pad;
     if (grid <= 0) return hipSuccess;
     if (grid > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((gemm_mfma_kernel<T, MODE, BM, BN>), dim3((unsigned)grid), dim3(kThreads),
-                       0, s, a);
+    hipLaunchKernelGGL((gemm_mfma_kernel<T, MODE, BM, BN, kBK, kStages>), dim3((unsigned)grid),
+                       dim3(kThreads), 0, s, a);
     return hipGetLastError();
 }
 
