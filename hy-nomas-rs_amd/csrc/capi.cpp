@@ -2,6 +2,7 @@
 //
 // Each one validates its arguments before touching the GPU, so configuration
 // errors are reported the same way on hosts without a device.
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -144,10 +145,12 @@ int nomas_moe_from_safetensors(const nomas_moe_config* cfg, const char* const* f
     std::map<std::string, nomas::StTensor> ts;
     rc = nomas::read_safetensors(fl, names, &ts);
     if (rc != NOMAS_OK) return rc;
-    // Missing keys are an error, listing the first few (weights.rs:117-127).
+    // Missing keys are an error, listing the first few in sorted order
+    // (weights.rs:117-127).
     std::vector<std::string> missing;
     for (const std::string& n : names)
         if (!ts.count(n)) missing.push_back(n);
+    std::sort(missing.begin(), missing.end());
     if (!missing.empty()) {
         std::string list;
         for (size_t i = 0; i < missing.size() && i < 5; ++i) list += (i ? ", " : "") + missing[i];

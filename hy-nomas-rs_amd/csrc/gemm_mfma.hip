@@ -25,11 +25,11 @@
 //    packed (rows 64g..64g+31 = gate 32g.., rows 64g+32.. = up 32g..), so a
 //    wave holds gate and up of the same hidden unit in the same lane and the
 //    SwiGLU is applied in the epilogue without an extra pass over HBM.
-//  - Tiles are ordered in groups of kGroupM row tiles (column index fastest
-//    within a group) and the grid is remapped so each XCD (block i runs on XCD
-//    i % 8) gets one contiguous range of that order: its concurrently running
-//    blocks share weight and token panels in the XCD's own L2.
+//  - Block ids are mapped to tiles XCD-aware (tile_map.hpp): the XCDs work on
+//    one expert at a time (its weights shared through the MALL), each XCD on a
+//    4 x 8 group of tiles that share panels in its own L2.
 #include "kernels.hpp"
+#include "tile_map.hpp"
 
 namespace nomas {
 
@@ -56,12 +56,8 @@ template <> struct Mfma<_Float16> {
 enum { kGateUp = 0, kDown = 1 };
 
 constexpr int kThreads = 256;
-constexpr int kGroupM = 4;
 constexpr int kBK = 32;     // k step
-#ifndef NOMAS_GEMM_STAGES
-#define NOMAS_GEMM_STAGES 4
-#endif
-constexpr int kStages = NOMAS_GEMM_STAGES;  // LDS ring depth
+constexpr int kStages = 4;  // LDS ring depth
 
 // Physical 16-byte chunk of logical chunk c in LDS row r (CH chunks per row).
 template <int CH>
@@ -80,40 +76,19 @@ __device__ __forceinline__ void wait_vmcnt() {
 // state between the M0 write and the load).  Issued as inline assembly so the
 // compiler does not track it: completion is waited for explicitly with
 // wait_vmcnt, and nothing else in these kernels uses M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // M0 is clobbered on purpose, see above
 __device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds_base) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                  :
                  : "v"(gptr), "s"(lds_base)
                  : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 template <typename P>
 __device__ __forceinline__ uint32_t lds_addr(P* p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
-}
-
-// Maps the hardware block id to (row tile, column tile); returns false for
-// padding blocks.  Blocks are dispatched in id order, block i to XCD i % 8,
-// so one XCD's queue is ids x, x+8, ...  Its k-th group of kCusPerXcd
-// consecutive queue entries ("round") runs roughly at time k.  Round
-// R = k * 8 + x takes logical tiles [R * kCusPerXcd, (R + 1) * kCusPerXcd):
-// at any time the eight XCDs work on eight consecutive rounds (the same
-// expert's weights, shared through the MALL), and inside an XCD a round is a
-// kGroupM x 8 block of tiles sharing panels in that XCD's L2.  The grid is
-// padded to a multiple of 8 * kCusPerXcd.
-constexpr int kCusPerXcd = 32;
-__device__ __forceinline__ bool tile_coords(int pid, int ntn, int max_tiles, int* mt, int* nt) {
-    const int xcd = pid % kNumXcd, loc = pid / kNumXcd;
-    const int round = (loc / kCusPerXcd) * kNumXcd + xcd;
-    const int L = round * kCusPerXcd + loc % kCusPerXcd;
-    const int group = L / (kGroupM * ntn);
-    const int first_m = group * kGroupM;
-    if (first_m >= max_tiles) return false;
-    const int gm = min(kGroupM, max_tiles - first_m);
-    const int within = L - group * kGroupM * ntn;
-    *mt = first_m + within % gm;
-    *nt = within / gm;
-    return true;
 }
 
 template <typename T, int MODE, int BM, int BN, int BK, int S>
@@ -327,8 +302,7 @@ template <typename T, int MODE>
 hipError_t launch_mfma_t(const GemmArgs& a, hipStream_t s) {
     constexpr int BM = kMfmaBM, BN = kMfmaBN;
     if (a.N % BN != 0 || a.K % (kBK * kStages) != 0) return hipErrorInvalidValue;
-    constexpr int64_t pad = (int64_t)kNumXcd * kCusPerXcd;
-    const int64_t grid = ((int64_t)a.max_tiles * (a.N / BN) + pad - 1) / pad * pad;
+    const int64_t grid = tile_grid(a.max_tiles, a.N / BN);
     if (grid <= 0) return hipSuccess;
     if (grid > 0x7fffffff) return hipErrorInvalidValue;
     hipLaunchKernelGGL((gemm_mfma_kernel<T, MODE, BM, BN, kBK, kStages>), dim3((unsigned)grid),

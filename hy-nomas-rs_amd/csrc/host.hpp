@@ -130,6 +130,10 @@ private:
 
     int64_t last_rows_ = -1;
     hipStream_t last_stream_ = nullptr;
+    // recorded at the end of every forward: a forward on another stream waits
+    // for it, since both use the same workspace
+    hipEvent_t done_ = nullptr;
+    bool done_recorded_ = false;
 
     // profiling: one set of 7 events per recorded forward
     bool profiling_ = false;

@@ -97,6 +97,7 @@ MoeLayer::~MoeLayer() {
     for (void* p : {d_wr_, d_w1_, (void*)d_b1_, d_w2_, (void*)d_b2_})
         if (p) (void)hipFree(p);
     for (hipEvent_t e : events_) (void)hipEventDestroy(e);
+    if (done_) (void)hipEventDestroy(done_);
 }
 
 int64_t MoeLayer::n_params() const {
@@ -304,6 +305,7 @@ int MoeLayer::forward(const void* x, void* y, int64_t rows, hipStream_t s) {
     if (!g.ok) return set_error(NOMAS_ERR_HIP, "hipSetDevice(%d) failed", device_);
     int rc = ensure_workspace(rows);
     if (rc != NOMAS_OK) return rc;
+    if (done_recorded_ && s != last_stream_) HIP_TRY(hipStreamWaitEvent(s, done_, 0));
 
     const int nch = (int)((rows + kRouterRows - 1) / kRouterRows);
     const int mt = max_tiles(rows);
@@ -407,6 +409,9 @@ int MoeLayer::forward(const void* x, void* y, int64_t rows, hipStream_t s) {
     STAGE(launch_combine(dt_, ca, s), "combine");
     if ((rc = mark(6))) return rc;
 #undef STAGE
+    if (!done_) HIP_TRY(hipEventCreateWithFlags(&done_, hipEventDisableTiming));
+    HIP_TRY(hipEventRecord(done_, s));
+    done_recorded_ = true;
     last_rows_ = rows;
     last_stream_ = s;
     return NOMAS_OK;

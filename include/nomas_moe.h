@@ -18,8 +18,11 @@
  *  - Weights use the reference's (out, in) layout with experts concatenated:
  *    router (E, D); gate/up (E, H, D) + bias (E, H); down (E, D, H) + bias (E, D).
  *  - dtype codes follow nomas-core/src/config.rs:30-39 (DataType).
- *  - A handle owns its device weights and workspace.  Calls on one handle
- *    are not re-entrant: use one handle per concurrent stream.
+ *  - A handle owns its device weights and workspace.  Forwards on one handle
+ *    are ordered: one issued on a different stream than the previous one
+ *    waits (on the device) for it to finish, since they share the workspace.
+ *    A handle must not be called from several host threads at once; use one
+ *    handle per thread for concurrency.
  */
 #ifndef NOMAS_MOE_H
 #define NOMAS_MOE_H

@@ -52,7 +52,6 @@ enum {
     MUT_DOWN_TRANSPOSED = 6,  /* down weight indexed (in, out) instead of (out, in) */
     MUT_FNV_PRIME = 7,        /* FNV-1a with a wrong multiplier                 */
     MUT_SPLITMIX_SHIFT = 8,   /* SplitMix64 first xor-shift 31 instead of 30    */
-    MUT_COMBINE_DESC = 9,     /* combine over experts in descending order (f32 only) */
 };
 
 /* ------------------------------------------------------------------ */
@@ -441,7 +440,7 @@ int orc_forward_dense_f32(int64_t T, int64_t D, int64_t E, int64_t k, int64_t H,
     if (w_dense) memcpy(w_dense, wts, sizeof(float) * (size_t)(T * E));
     memset(out, 0, sizeof(float) * (size_t)(T * D));
     for (int64_t ei = 0; ei < E; ++ei) {
-        int64_t e = orc_mutation == MUT_COMBINE_DESC ? E - 1 - ei : ei;
+        int64_t e = ei;
         swiglu_dense_f32(T, D, H, x, wg + e * H * D, bg ? bg + e * H : NULL, wu + e * H * D,
                          bu ? bu + e * H : NULL, wd + e * D * H, bd ? bd + e * D : NULL, G, U, Y);
 #pragma omp parallel for schedule(static)

@@ -79,7 +79,6 @@ MUTATIONS = {
     "down_transposed": 6,
     "fnv_prime": 7,
     "splitmix_shift": 8,
-    "combine_desc": 9,
 }
 
 

@@ -1,0 +1,163 @@
+"""The C ABI (include/nomas_moe.h) on the host -- CPU only.
+
+Loads libnomas_moe.so, checks that it exports every declared entry point, and
+exercises every error path that is decided before the GPU is touched: config
+validation (config.rs:394-399), shape limits, null arguments, and checkpoint
+loading (weights.rs:105-145: missing keys, misshaped tensors, unreadable files).
+"""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+from safetensors.numpy import save_file
+
+import nomas_moe as nm
+from nomas_moe import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "nomas_moe.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nomas_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_entry_point():
+    L = _lib.lib()
+    names = declared_functions()
+    assert len(names) >= 18
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_config_validate_mirrors_reference():
+    nm.MoeConfig(experts=8, top_k=2).validate()
+    nm.MoeConfig(experts=4, top_k=4).validate()
+    for bad in (nm.MoeConfig(4, 0), nm.MoeConfig(4, 5), nm.MoeConfig(0, 1)):
+        with pytest.raises(nm.InvalidConfig, match="invalid MoE top_k/experts"):
+            bad.validate()
+
+
+@pytest.mark.parametrize("cfg,dim,hidden,dtype,msg", [
+    (nm.MoeConfig(4, 5), 64, 128, 0, "top_k"),
+    (nm.MoeConfig(300, 2), 64, 128, 0, "maximum"),
+    (nm.MoeConfig(4, 2), 60, 128, 0, "multiple of 8"),
+    (nm.MoeConfig(4, 2), 64, 0, 0, "hidden"),
+    (nm.MoeConfig(4, 2), 64, 128, 7, "dtype"),
+])
+def test_create_rejects_invalid_config_before_touching_the_gpu(cfg, dim, hidden, dtype, msg):
+    h = C.c_void_p()
+    c = cfg._c()
+    rc = _lib.lib().nomas_moe_from_random(C.byref(c), b"blocks.0.moe", dim, hidden, dtype, 1, 0,
+                                          C.byref(h))
+    assert rc == 1, _lib.last_error()
+    assert msg in _lib.last_error()
+    assert not h.value
+
+
+def test_null_arguments_are_rejected():
+    L = _lib.lib()
+    c = nm.MoeConfig(4, 2)._c()
+    h = C.c_void_p()
+    assert L.nomas_moe_from_random(None, b"p", 64, 128, 0, 1, 0, C.byref(h)) == 2
+    assert L.nomas_moe_from_random(C.byref(c), None, 64, 128, 0, 1, 0, C.byref(h)) == 2
+    assert L.nomas_moe_from_host(C.byref(c), 64, 128, 0, 0, *([None] * 13), C.byref(h)) == 2
+    assert L.nomas_moe_forward(None, None, None, 4, None) == 2
+    assert L.nomas_moe_forward_host(None, None, None, 4) == 2
+    assert L.nomas_moe_routing(None, None, None, None, None) == 2
+    assert L.nomas_moe_n_params(None) == -1
+    assert L.nomas_moe_uses_mfma(None) == 0
+    L.nomas_moe_destroy(None)  # no-op
+
+
+def _checkpoint(path, E, D, H, dtype=np.float32, drop=(), reshape=None, dense=False):
+    rng = np.random.default_rng(0)
+    t = {"blocks.0.moe.router.weight": rng.standard_normal((E, D)).astype(dtype)}
+    names = [f"blocks.0.moe.experts.{e}" for e in range(E)] + (["blocks.0.moe.dense"] if dense else [])
+    for base in names:
+        for lin, (o, i) in (("gate", (H, D)), ("up", (H, D)), ("down", (D, H))):
+            t[f"{base}.{lin}.weight"] = rng.standard_normal((o, i)).astype(dtype)
+            t[f"{base}.{lin}.bias"] = rng.standard_normal(o).astype(dtype)
+    t["blocks.0.attn.q.weight"] = np.zeros((2, 2), dtype)  # unrelated keys are ignored
+    for k in drop:
+        del t[k]
+    if reshape:
+        t[reshape] = t[reshape].reshape(-1)
+    save_file(t, path)
+    return t
+
+
+def _load(files, E=2, k=1, D=16, H=8, dtype=0, s=0.0):
+    c = nm.MoeConfig(E, k, s)._c()
+    arr = (C.c_char_p * len(files))(*[f.encode() for f in files])
+    h = C.c_void_p()
+    rc = _lib.lib().nomas_moe_from_safetensors(C.byref(c), arr, len(files), b"blocks.0.moe", D, H,
+                                               dtype, 0, C.byref(h))
+    return rc, _lib.last_error()
+
+
+def test_checkpoint_missing_expert_keys(tmp_path):
+    # weights.rs:175-188 (moe_keys): with 2 experts, experts.1.* exist and
+    # experts.2.* do not; asking for 3 experts reports the missing keys
+    f = str(tmp_path / "moe.safetensors")
+    _checkpoint(f, 2, 16, 8)
+    rc, msg = _load([f], E=3, k=1)
+    assert rc == 3
+    assert "blocks.0.moe.experts.2.down.bias" in msg and "missing 6 model keys" in msg
+
+
+def test_checkpoint_missing_router(tmp_path):
+    f = str(tmp_path / "moe.safetensors")
+    _checkpoint(f, 2, 16, 8, drop=("blocks.0.moe.router.weight",))
+    rc, msg = _load([f])
+    assert rc == 3 and "router.weight" in msg
+
+
+def test_checkpoint_misshaped_tensor(tmp_path):
+    f = str(tmp_path / "moe.safetensors")
+    _checkpoint(f, 2, 16, 8, reshape="blocks.0.moe.experts.1.up.weight")
+    rc, msg = _load([f])
+    assert rc == 3 and "experts.1.up.weight" in msg
+
+
+def test_checkpoint_dense_branch_keys_required_when_shared_dense(tmp_path):
+    f = str(tmp_path / "moe.safetensors")
+    _checkpoint(f, 2, 16, 8, dense=False)
+    rc, msg = _load([f], s=0.5)
+    assert rc == 3 and "blocks.0.moe.dense" in msg
+
+
+def test_checkpoint_unreadable(tmp_path):
+    rc, msg = _load([str(tmp_path / "nope.safetensors")])
+    assert rc == 4 and "cannot open" in msg
+    bad = tmp_path / "bad.safetensors"
+    bad.write_bytes(b"\x10\x00\x00\x00\x00\x00\x00\x00{not json at all")
+    rc, msg = _load([str(bad)])
+    assert rc == 4
+
+
+def test_complete_checkpoint_parses_then_needs_a_device(tmp_path):
+    # every key present and well-formed: loading proceeds to device creation
+    f = str(tmp_path / "moe.safetensors")
+    _checkpoint(f, 2, 16, 8, dtype=np.float16)
+    rc, msg = _load([f])
+    import torch
+    if torch.cuda.is_available():
+        assert rc == 0, msg
+    else:
+        assert rc == 5 and "HIP device" in msg
+
+
+def test_dtype_helpers_round_to_nearest_even():
+    import torch
+    x = np.concatenate([nm.randn_affine(3, 5000, 0.0, 30.0),
+                        np.array([1.00390625, -65519.0, 65520.0, 6e-8, 1e-40], np.float32)])
+    bf = nm.to_model_dtype(x, "bf16")
+    np.testing.assert_array_equal(nm.widen(bf, "bf16"),
+                                  torch.from_numpy(x).to(torch.bfloat16).float().numpy())
+    hf = nm.to_model_dtype(x, "f16")
+    np.testing.assert_array_equal(nm.widen(hf, "f16"), x.astype(np.float16).astype(np.float32))
