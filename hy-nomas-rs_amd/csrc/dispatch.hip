@@ -167,10 +167,15 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(DispatchArgs a) {
         const T* src = x + (row0 + r) * (int64_t)a.D;
         for (int c = lane; c < nchunk; c += kWave) {
             const uint4 v = *reinterpret_cast<const uint4*>(src + (int64_t)c * EPC);
+            const int64_t col = (int64_t)c * EPC;
             for (int j = 0; j < k; ++j) {
                 const int p = s_pos[r * k + j];
-                if (p >= 0 && p < a.a_cap)
-                    *reinterpret_cast<uint4*>(xp + (int64_t)p * a.D + (int64_t)c * EPC) = v;
+                if (p < 0 || p >= a.a_cap) continue;
+                // row-major (p, col) or K-blocked ((col / 32) * a_cap + p) * 32 + col % 32
+                const int64_t off = a.kblocked
+                    ? ((col / kKBlock) * a.a_cap + p) * kKBlock + col % kKBlock
+                    : (int64_t)p * a.D + col;
+                *reinterpret_cast<uint4*>(xp + off) = v;
             }
         }
     }

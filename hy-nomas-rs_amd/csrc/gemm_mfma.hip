@@ -17,6 +17,8 @@
 //    direct global->LDS loads (global_load_lds_dwordx4: no VGPR staging).
 //    Loads run S-1 steps ahead of the MFMAs; each step waits only for its own
 //    stage (partial vmcnt) and synchronises the block once.
+//  - Operands are K-blocked in memory (kernels.hpp): one k step of a tile is a
+//    single contiguous 16 KB run, fetched as whole 128-byte lines.
 //  - LDS rows (BK * 2 bytes) keep their 16-byte chunks XOR-swizzled, so the
 //    32-row MFMA operand reads (ds_read_b128) are free of bank conflicts.  The
 //    swizzle is applied on the global side: lane l of a load instruction always
@@ -105,6 +107,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
     static_assert(MODE == kDown || SN % 2 == 0, "gate/up pairs need an even block count");
     static_assert(S >= 3 && S <= 5, "ring depth");
     static_assert((S - 2) * Q <= 63, "vmcnt range");
+    static_assert(BK == kKBlock, "operands are K-blocked by the k step");
 
     // One LDS object per stage: the compiler then knows a stage being read is
     // not the target of the loads in flight, and inserts no vmcnt(0) before
@@ -133,8 +136,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
 
-    const T* Wt = static_cast<const T*>(a.W) + ((int64_t)e * N + n0) * K;
-    const T* Xt = static_cast<const T*>(a.X) + (int64_t)row0 * K;
+    // K-blocked operands: step kt of this tile is one contiguous block of
+    // 256 rows x BK for the weights (stride N * BK between steps) and for the
+    // token rows (stride a_cap * BK).
+    const T* Wt = static_cast<const T*>(a.W) + ((int64_t)e * (K / BK) * N + n0) * BK;
+    const T* Xt = static_cast<const T*>(a.X) + (int64_t)row0 * BK;
+    const int64_t wstep = (int64_t)N * BK, xstep = a.a_cap * BK;
 
     // Lane l of load instruction q writes LDS bytes [q*1024 + l*16, +16): tile
     // row r = RPI*q + l/CH, stored chunk l%CH, which holds logical chunk
@@ -143,13 +150,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < QW; ++i) {
         const int r = (wave * QW + i) * RPI + lane / CH;
-        woff[i] = r * K + (((lane % CH) ^ swz<CH>(r)) * 8);
+        woff[i] = r * BK + (((lane % CH) ^ swz<CH>(r)) * 8);
     }
 #pragma unroll
     for (int i = 0; i < QX; ++i) {
         const int r = (wave * QX + i) * RPI + lane / CH;
         const int rr = r < nrows ? r : nrows - 1;
-        xoff[i] = rr * K + (((lane % CH) ^ swz<CH>(r)) * 8);
+        xoff[i] = rr * BK + (((lane % CH) ^ swz<CH>(r)) * 8);
     }
 
     f32x16_t acc[SN][SM];
@@ -162,15 +169,16 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
 
     const int uwave = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform (SGPR) copy
     auto issue = [&](int kt, int buf) {
-        const int ko = kt * BK;
+        const T* ws = Wt + kt * wstep;
+        const T* xs = Xt + kt * xstep;
         const uint32_t bw = lds_addr(stW(buf)) + uwave * QW * RPI * BK * (int)sizeof(T);
         const uint32_t bx = lds_addr(stX(buf)) + uwave * QX * RPI * BK * (int)sizeof(T);
 #pragma unroll
         for (int i = 0; i < QW; ++i)
-            lds_dma16(Wt + woff[i] + ko, bw + i * RPI * BK * (int)sizeof(T));
+            lds_dma16(ws + woff[i], bw + i * RPI * BK * (int)sizeof(T));
 #pragma unroll
         for (int i = 0; i < QX; ++i)
-            lds_dma16(Xt + xoff[i] + ko, bx + i * RPI * BK * (int)sizeof(T));
+            lds_dma16(xs + xoff[i], bx + i * RPI * BK * (int)sizeof(T));
         // keep the loads ahead of the MFMAs that follow
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -185,7 +193,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
     auto compute_issue = [&](int buf, int ktl, int bufl) {
         const T* cW = stW(buf);
         const T* cX = stX(buf);
-        const int ko = ktl * BK;
+        const T* ws = Wt + ktl * wstep;
+        const T* xs = Xt + ktl * xstep;
         const uint32_t bw = lds_addr(stW(bufl)) + uwave * QW * RPI * BK * (int)sizeof(T);
         const uint32_t bx = lds_addr(stX(bufl)) + uwave * QX * RPI * BK * (int)sizeof(T);
 #pragma unroll
@@ -209,8 +218,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
                     const int m = (ks * SN + i) * SM + j;  // compile-time after unrolling
                     if (m % EVERY == 0) {
                         const int q = m / EVERY;
-                        if (q < QW) lds_dma16(Wt + woff[q] + ko, bw + q * RPI * BK * (int)sizeof(T));
-                        else lds_dma16(Xt + xoff[q - QW] + ko, bx + (q - QW) * RPI * BK * (int)sizeof(T));
+                        if (q < QW) lds_dma16(ws + woff[q], bw + q * RPI * BK * (int)sizeof(T));
+                        else lds_dma16(xs + xoff[q - QW], bx + (q - QW) * RPI * BK * (int)sizeof(T));
                     }
                     acc[i][j] = Mfma<T>::run(av[i], bv[j], acc[i][j]);
                 }
@@ -251,8 +260,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
         const int m = wm * WM + j * 32 + l32;
         if (m >= nrows) continue;
         if (MODE == kGateUp) {
-            const int H = N / 2;
-            T* orow = out + (int64_t)(row0 + m) * H;
+            // h is written K-blocked for the down GEMM: (row, c) at
+            // ((c / 32) * a_cap + row) * 32 + c % 32
+            T* hrow = out + (int64_t)(row0 + m) * kKBlock;
 #pragma unroll
             for (int q = 0; q < SN / 2; ++q) {
                 const int pbase = n0 + wn * WN + q * 64;  // packed row of gate unit 0 of the pair
@@ -272,7 +282,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
                     }
                     uint2 raw;
                     __builtin_memcpy(&raw, hv, 8);
-                    *reinterpret_cast<uint2*>(orow + pbase / 2 + off) = raw;
+                    const int hc = pbase / 2 + off;  // 4 columns inside one 32-block
+                    *reinterpret_cast<uint2*>(hrow + (int64_t)(hc / kKBlock) * a.a_cap * kKBlock +
+                                              hc % kKBlock) = raw;
                 }
             }
         } else {

@@ -46,6 +46,13 @@ struct ScanArgs {
     int32_t* tile_total;    // 1
 };
 
+// K-blocked layout (MFMA path): a matrix of R rows and K columns is stored as
+// K / kKBlock column blocks, each R rows x kKBlock contiguous elements, i.e.
+// element (r, k) at ((k / kKBlock) * R + r) * kKBlock + k % kKBlock.  One
+// k step of a GEMM tile (256 rows x kKBlock) is then a single contiguous 16 KB
+// run of memory, fetched as whole 128-byte lines.
+constexpr int kKBlock = 32;
+
 struct DispatchArgs {
     const void* x;
     int64_t rows;
@@ -53,12 +60,13 @@ struct DispatchArgs {
     const int32_t* topk_idx;
     const int32_t* chunk_base;
     int32_t* tok_pos;  // rows x k_slots
-    void* x_perm;      // A x D
+    void* x_perm;      // a_cap x D, row-major or K-blocked
     int64_t a_cap;     // rows of x_perm (positions must stay below)
+    int kblocked;      // 1: write x_perm K-blocked (R = a_cap), 0: row-major
 };
 
 struct GemmArgs {
-    const void* X;     // token rows (A x K), expert-contiguous
+    const void* X;     // token rows (a_cap x K), expert-contiguous
     const void* W;     // expert weights
     const float* bias; // expert biases (f32)
     void* out;

@@ -156,7 +156,14 @@ int MoeLayer::upload(const void* router_w, const void* gate_w, const void* gate_
                 src_row = p % H;
             }
             const uint8_t* src = (is_up ? uw : gw) + src_row * D * es;
-            std::memcpy(&w1[(size_t)((e * 2 * H + p) * D) * es], src, (size_t)D * es);
+            if (mfma_) {  // K-blocked: (e, p, k) at ((e * D/32 + k/32) * 2H + p) * 32 + k % 32
+                const int64_t KB = D / kKBlock;
+                for (int64_t kb = 0; kb < KB; ++kb)
+                    std::memcpy(&w1[(size_t)(((e * KB + kb) * 2 * H + p) * kKBlock) * es],
+                                src + kb * kKBlock * es, (size_t)kKBlock * es);
+            } else {
+                std::memcpy(&w1[(size_t)((e * 2 * H + p) * D) * es], src, (size_t)D * es);
+            }
             b1[(size_t)(e * 2 * H + p)] = is_up ? bsrc(up_b, du_b, e, H, src_row)
                                                 : bsrc(gate_b, dg_b, e, H, src_row);
         }
@@ -165,7 +172,16 @@ int MoeLayer::upload(const void* router_w, const void* gate_w, const void* gate_
     std::vector<uint8_t> w2((size_t)(Ecols_ * D * H) * es);
     std::vector<float> b2((size_t)(Ecols_ * D));
     for (int64_t e = 0; e < Ecols_; ++e) {
-        std::memcpy(&w2[(size_t)(e * D * H) * es], wsrc(down_w, dd_w, e, D * H), (size_t)(D * H) * es);
+        const uint8_t* src = wsrc(down_w, dd_w, e, D * H);
+        if (mfma_) {  // K-blocked: (e, n, k) at ((e * H/32 + k/32) * D + n) * 32 + k % 32
+            const int64_t KB = H / kKBlock;
+            for (int64_t n = 0; n < D; ++n)
+                for (int64_t kb = 0; kb < KB; ++kb)
+                    std::memcpy(&w2[(size_t)(((e * KB + kb) * D + n) * kKBlock) * es],
+                                src + (n * H + kb * kKBlock) * es, (size_t)kKBlock * es);
+        } else {
+            std::memcpy(&w2[(size_t)(e * D * H) * es], src, (size_t)(D * H) * es);
+        }
         for (int64_t d = 0; d < D; ++d) b2[(size_t)(e * D + d)] = bsrc(down_b, dd_b, e, D, d);
     }
 
@@ -367,6 +383,7 @@ int MoeLayer::forward(const void* x, void* y, int64_t rows, hipStream_t s) {
     da.tok_pos = d_pos_;
     da.x_perm = d_xperm_;
     da.a_cap = cap_rows_ * kslots_;
+    da.kblocked = mfma_ ? 1 : 0;
     STAGE(launch_dispatch(dt_, da, s), "dispatch");
     if ((rc = mark(3))) return rc;
 
