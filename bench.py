@@ -39,6 +39,34 @@ def algorithmic(w, b):
     }
 
 
+def traffic_from_profile(workload):
+    """HBM bytes per launch of the gate/up GEMM, from the committed rocprofv3
+    counter summary (FETCH_SIZE + WRITE_SIZE, calibrated against a copy of
+    known size), or None when no summary for this workload exists."""
+    path = os.path.join(ROOT, "profiles", f"gemm_gate_up_{workload}_hbm_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("hbm_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def copy_probe(mb):
+    """A plain device copy of known size (f16 -> f32 conversion: reads 2 bytes
+    and writes 4 bytes per element), used to calibrate the FETCH_SIZE and
+    WRITE_SIZE counters."""
+    import torch
+    n = mb * (1 << 20) // 2
+    src = torch.ones(n, dtype=torch.float16, device="cuda")
+    dst = torch.empty(n, dtype=torch.float32, device="cuda")
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_elements": n, "read_bytes": 2 * n, "write_bytes": 4 * n}))
+    return 0
+
+
 def cpu_baseline(w, params, x, target_s=12.0):
     """The reference algorithm (every expert on every row, f32) on host cores,
     timed on a bounded prefix of the workload's rows."""
@@ -73,7 +101,11 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="cfg8b")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe-mb", type=int, default=0,
+                    help="only run a plain copy of this many MB (counter calibration) and exit")
     args = ap.parse_args()
+    if args.copy_probe_mb:
+        return copy_probe(args.copy_probe_mb)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: the MoE "
               "feed-forward path here is single-GPU (no collectives).", file=sys.stderr)
@@ -145,7 +177,7 @@ def main() -> int:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": gu_tf / PEAK_BF16_TFLOPS,
-            "traffic": None,
+            "traffic": traffic_from_profile(w.name),
         },
         "stages_ms": stages,
         "gemm_tflops": {"gate_up": gu_tf, "down": dn_tf, "both": both_tf,

@@ -73,17 +73,18 @@ __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// Direct global->LDS load of 16 bytes per lane: lane l's bytes land at LDS
-// address lds_base + 16 * l (global_load_lds_dwordx4, M0 = LDS base; one wait
-// state between the M0 write and the load).  Issued as inline assembly so the
-// compiler does not track it: completion is waited for explicitly with
-// wait_vmcnt, and nothing else in these kernels uses M0.
+// Direct global->LDS load of 16 bytes per lane from sbase + voff (a uniform
+// 64-bit base in SGPRs plus a per-lane 32-bit byte offset): lane l's bytes
+// land at LDS address lds_base + 16 * l (global_load_lds_dwordx4, M0 = LDS
+// base; one wait state between the M0 write and the load).  Issued as inline
+// assembly so the compiler does not track it: completion is waited for
+// explicitly with wait_vmcnt, and nothing else in these kernels uses M0.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"  // M0 is clobbered on purpose, see above
-__device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+__device__ __forceinline__ void lds_dma16(const void* sbase, uint32_t voff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                  :
-                 : "v"(gptr), "s"(lds_base)
+                 : "v"(voff), "s"(sbase), "s"(lds_base)
                  : "memory", "m0");
 }
 #pragma clang diagnostic pop
@@ -150,13 +151,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < QW; ++i) {
         const int r = (wave * QW + i) * RPI + lane / CH;
-        woff[i] = r * BK + (((lane % CH) ^ swz<CH>(r)) * 8);
+        woff[i] = (r * BK + (((lane % CH) ^ swz<CH>(r)) * 8)) * (int)sizeof(T);  // bytes
     }
 #pragma unroll
     for (int i = 0; i < QX; ++i) {
         const int r = (wave * QX + i) * RPI + lane / CH;
         const int rr = r < nrows ? r : nrows - 1;
-        xoff[i] = rr * BK + (((lane % CH) ^ swz<CH>(r)) * 8);
+        xoff[i] = (rr * BK + (((lane % CH) ^ swz<CH>(r)) * 8)) * (int)sizeof(T);  // bytes
     }
 
     f32x16_t acc[SN][SM];
@@ -175,10 +176,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
         const uint32_t bx = lds_addr(stX(buf)) + uwave * QX * RPI * BK * (int)sizeof(T);
 #pragma unroll
         for (int i = 0; i < QW; ++i)
-            lds_dma16(ws + woff[i], bw + i * RPI * BK * (int)sizeof(T));
+            lds_dma16(ws, woff[i], bw + i * RPI * BK * (int)sizeof(T));
 #pragma unroll
         for (int i = 0; i < QX; ++i)
-            lds_dma16(xs + xoff[i], bx + i * RPI * BK * (int)sizeof(T));
+            lds_dma16(xs, xoff[i], bx + i * RPI * BK * (int)sizeof(T));
         // keep the loads ahead of the MFMAs that follow
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -218,8 +219,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
                     const int m = (ks * SN + i) * SM + j;  // compile-time after unrolling
                     if (m % EVERY == 0) {
                         const int q = m / EVERY;
-                        if (q < QW) lds_dma16(ws + woff[q], bw + q * RPI * BK * (int)sizeof(T));
-                        else lds_dma16(xs + xoff[q - QW], bx + (q - QW) * RPI * BK * (int)sizeof(T));
+                        if (q < QW) lds_dma16(ws, woff[q], bw + q * RPI * BK * (int)sizeof(T));
+                        else lds_dma16(xs, xoff[q - QW], bx + (q - QW) * RPI * BK * (int)sizeof(T));
                     }
                     acc[i][j] = Mfma<T>::run(av[i], bv[j], acc[i][j]);
                 }

@@ -6,7 +6,7 @@
 
 namespace nomas {
 
-constexpr int kTileGroupM = 4;   // row tiles per group (column index fastest inside)
+constexpr int kTileGroupM = 8;   // row tiles per group (row index fastest inside)
 constexpr int kXcds = 8;         // MI355X: 8 XCDs
 constexpr int kCusPerXcd = 32;   // 32 CUs per XCD
 
