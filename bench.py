@@ -80,7 +80,7 @@ def cpu_baseline(w, params, x, target_s=12.0):
     t0 = time.perf_counter()
     O.forward_dense_f32(x[:probe], p, w.top_k)
     dt = time.perf_counter() - t0
-    rows = int(max(probe, min(w.rows, 1024, probe * target_s / max(dt, 1e-3))))
+    rows = int(max(probe, min(w.rows, probe * target_s / max(dt, 1e-3))))
     t0 = time.perf_counter()
     O.forward_dense_f32(x[:rows], p, w.top_k)
     dt = time.perf_counter() - t0

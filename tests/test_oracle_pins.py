@@ -71,6 +71,19 @@ def pin_affine_and_moments():
     np.testing.assert_allclose(a, (z[:1000] * 0.5 + 3.0).astype(np.float32), rtol=0, atol=5e-7)
 
 
+def pin_uniform():
+    # deterministic_uniform (tensor_utils.rs:140-155): one 53-bit draw per
+    # element, mapped affinely onto [lo, hi); range and the U(lo, hi) moments
+    # hold independently of how the draw is formed
+    lo, hi, n = -0.5, 1.5, 100_000
+    u = O.uniform(31, n, lo, hi).astype(np.float64)
+    assert u.min() >= lo and u.max() < hi
+    assert abs(u.mean() - (lo + hi) / 2) < 5 * (hi - lo) / math.sqrt(12 * n)
+    assert abs(u.var() - (hi - lo) ** 2 / 12) < 0.01 * (hi - lo) ** 2 / 12
+    want = np.array([lo + d * (hi - lo) for d in _uniform_draws(31, 64)], np.float32)
+    np.testing.assert_array_equal(u[:64].astype(np.float32), want)
+
+
 def pin_xavier_std():
     w = O.xavier(256, 192, 9).astype(np.float64)
     want = math.sqrt(2.0 / (256 + 192))
@@ -261,7 +274,8 @@ def pin_shared_dense_branch():
     np.testing.assert_allclose(got, want, rtol=1e-10, atol=1e-12)
 
 
-PINS = [pin_splitmix64, pin_fnv1a, pin_box_muller, pin_affine_and_moments, pin_xavier_std,
+PINS = [pin_splitmix64, pin_fnv1a, pin_box_muller, pin_affine_and_moments, pin_uniform,
+        pin_xavier_std,
         pin_bf16_rounding, pin_route_bruteforce, pin_route_ties_lowest_index,
         pin_route_one_hot_rows, pin_route_weights_sum_to_one, pin_forward_bruteforce,
         pin_dense_equals_sparse, pin_k_equals_experts, pin_single_dominant_expert,
