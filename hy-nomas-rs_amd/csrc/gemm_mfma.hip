@@ -5,31 +5,33 @@
 //   down:     y[m, :] = h W_down^T + b_down                              K = H, N = D
 // (hy-nomas-rs mlp.rs:42-46 applied to the rows routed to e).
 //
-// Work unit: a BM x BN output tile of one expert.  The scan kernel lists the
-// experts' BM-row tiles; the grid enumerates (row tile, column tile) pairs.
+// Work unit: a 256 x 256 output tile of one expert.  The scan kernel lists
+// the experts' 256-row tiles; the grid enumerates (row tile, column tile).
 //  - Operands: weights are the MFMA "A" operand (rows = output columns),
 //    token rows the "B" operand, so each lane's accumulator holds 4
 //    consecutive output columns of one token row (8-byte stores).
-//  - v_mfma_f32_32x32x16_{bf16,f16}; 4 waves in a 2 x 2 grid, each wave a
-//    (BN/2) x (BM/2) tile of 32 x 32 MFMA blocks (256 f32 accumulators per
-//    lane for 256 x 256 tiles, held in AGPRs).
-//  - K is walked in BK-wide steps through a ring of S LDS stages filled by
-//    direct global->LDS loads (global_load_lds_dwordx4: no VGPR staging).
-//    Loads run S-1 steps ahead of the MFMAs; each step waits only for its own
-//    stage (partial vmcnt) and synchronises the block once.
-//  - Operands are K-blocked in memory (kernels.hpp): one k step of a tile is a
-//    single contiguous 16 KB run, fetched as whole 128-byte lines.
-//  - LDS rows (BK * 2 bytes) keep their 16-byte chunks XOR-swizzled, so the
-//    32-row MFMA operand reads (ds_read_b128) are free of bank conflicts.  The
-//    swizzle is applied on the global side: lane l of a load instruction always
-//    writes LDS slot l, and reads the global chunk that belongs there.
+//  - v_mfma_f32_16x16x32_{bf16,f16}: 4 waves in a 2 x 2 grid, each wave a
+//    128 x 128 tile of 8 x 8 MFMA blocks (256 f32 accumulators per lane, in
+//    AGPRs).  The 16x16x32 form does the same work per cycle as 32x32x16 for
+//    less power, which matters because these GEMMs run at the power limit.
+//  - K is walked 32 at a time (one MFMA k step) through a ring of 4 LDS
+//    stages filled by direct global->LDS loads (global_load_lds_dwordx4, no
+//    VGPR staging), issued 2-3 steps ahead.  Operands are K-blocked in memory
+//    (kernels.hpp): one k step of a tile is a single contiguous 16 KB run.
+//  - LDS rows (64 bytes) keep their 16-byte chunks XOR-swizzled by row bits
+//    1-2, so the 16-row operand reads (ds_read_b128) are free of bank
+//    conflicts, and one lane's read offset is the same for every block (the
+//    block index folds into the instruction's immediate offset).  The swizzle
+//    is applied on the global side: lane l of a load instruction always
+//    writes LDS slot l and reads the global chunk that belongs there.
 //  - Gate and up rows are interleaved in groups of 32 when the weights are
-//    packed (rows 64g..64g+31 = gate 32g.., rows 64g+32.. = up 32g..), so a
-//    wave holds gate and up of the same hidden unit in the same lane and the
-//    SwiGLU is applied in the epilogue without an extra pass over HBM.
+//    packed (rows 64g..64g+31 = gate 32g.., rows 64g+32.. = up 32g..), so
+//    gate block 4p+b and up block 4p+b+2 of a wave hold the same hidden units
+//    in the same lanes, and the SwiGLU is applied in the epilogue without an
+//    extra pass over HBM.
 //  - Block ids are mapped to tiles XCD-aware (tile_map.hpp): the XCDs work on
-//    one expert at a time (its weights shared through the MALL), each XCD on a
-//    4 x 8 group of tiles that share panels in its own L2.
+//    one expert at a time (its weights shared through the MALL), each XCD on
+//    an 8 x 4 group of tiles that share panels in its own L2.
 #include "kernels.hpp"
 #include "tile_map.hpp"
 
@@ -39,34 +41,32 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 template <typename T> struct Mfma;
 template <> struct Mfma<__bf16> {
     typedef bf16x8_t V;
-    static __device__ __forceinline__ f32x16_t run(V a, V b, f32x16_t c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    static __device__ __forceinline__ f32x4_t run(V a, V b, f32x4_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
     }
 };
 template <> struct Mfma<_Float16> {
     typedef f16x8_t V;
-    static __device__ __forceinline__ f32x16_t run(V a, V b, f32x16_t c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    static __device__ __forceinline__ f32x4_t run(V a, V b, f32x4_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
     }
 };
 
 enum { kGateUp = 0, kDown = 1 };
 
 constexpr int kThreads = 256;
-constexpr int kBK = 32;     // k step
-constexpr int kStages = 4;  // LDS ring depth
+constexpr int kBK = 32;     // k step = one 16x16x32 MFMA
+constexpr int kStages = 4;  // LDS ring depth; the main loop is unrolled over one turn
 
-// Physical 16-byte chunk of logical chunk c in LDS row r (CH chunks per row).
-template <int CH>
-__device__ __forceinline__ int swz(int r) {
-    if constexpr (CH == 8) return (r ^ (r >> 3)) & 7;
-    else return ((r >> 1) ^ (r >> 3)) & 3;
-}
+// Physical 16-byte chunk of logical chunk c in LDS row r is c ^ swz(r) (4
+// chunks per row).  Any 8 consecutive rows read at one logical chunk then hit
+// 8 distinct (row parity, chunk) bank groups.
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & 3; }
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -98,31 +98,27 @@ template <typename T, int MODE, int BM, int BN, int BK, int S>
 __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
     using V = typename Mfma<T>::V;
     constexpr int WM = BM / 2, WN = BN / 2;       // wave tile: token rows x weight rows
-    constexpr int SM = WM / 32, SN = WN / 32;     // 32x32 MFMA blocks per wave
+    constexpr int SM = WM / 16, SN = WN / 16;     // 16x16 MFMA blocks per wave
     constexpr int CH = BK / 8;                    // 16-byte chunks per LDS row
     constexpr int RPI = kWave / CH;               // rows filled by one load instruction
     constexpr int NW = kThreads / kWave;
     constexpr int QW = BN / RPI / NW;             // load instructions per wave per k step
     constexpr int QX = BM / RPI / NW;
     constexpr int Q = QW + QX;
-    static_assert(MODE == kDown || SN % 2 == 0, "gate/up pairs need an even block count");
-    static_assert(S >= 3 && S <= 5, "ring depth");
-    static_assert((S - 2) * Q <= 63, "vmcnt range");
+    static_assert(BK == 32 && CH == 4, "one 16x16x32 k step per stage");
+    static_assert(S == 4, "ring of 4 stages, the loop unrolled over one turn");
+    static_assert(SN == 8 && SM == 8 && Q == 8, "row schedule: 8 x 8 blocks, 8 loads per step");
+    static_assert(MODE == kDown || SN % 4 == 0, "gate/up pairs are 2 blocks apart in groups of 4");
     static_assert(BK == kKBlock, "operands are K-blocked by the k step");
 
-    // One LDS object per stage: the compiler then knows a stage being read is
-    // not the target of the loads in flight, and inserts no vmcnt(0) before
-    // the reads.  Stage indices are compile-time after unrolling.
-    __shared__ __attribute__((aligned(16))) T sW0[BN * BK], sW1[BN * BK], sW2[BN * BK],
-        sW3[S > 3 ? BN * BK : 8], sW4[S > 4 ? BN * BK : 8];
-    __shared__ __attribute__((aligned(16))) T sX0[BM * BK], sX1[BM * BK], sX2[BM * BK],
-        sX3[S > 3 ? BM * BK : 8], sX4[S > 4 ? BM * BK : 8];
-    auto stW = [&](int s) -> T* {
-        return s == 0 ? sW0 : s == 1 ? sW1 : s == 2 ? sW2 : s == 3 ? sW3 : sW4;
-    };
-    auto stX = [&](int s) -> T* {
-        return s == 0 ? sX0 : s == 1 ? sX1 : s == 2 ? sX2 : s == 3 ? sX3 : sX4;
-    };
+    // One LDS object per stage (indices are compile-time after unrolling).
+    __shared__ __attribute__((aligned(16))) T sW0[BN * BK], sW1[BN * BK], sW2[BN * BK], sW3[BN * BK];
+    __shared__ __attribute__((aligned(16))) T sX0[BM * BK], sX1[BM * BK], sX2[BM * BK], sX3[BM * BK];
+    // the tile's BN biases (f32), loaded by one direct-to-LDS instruction
+    __shared__ __attribute__((aligned(16))) float sBias[BN];
+    static_assert(BN * sizeof(float) == kWave * 16, "one 16-byte chunk per lane");
+    auto stW = [&](int s) -> T* { return s == 0 ? sW0 : s == 1 ? sW1 : s == 2 ? sW2 : sW3; };
+    auto stX = [&](int s) -> T* { return s == 0 ? sX0 : s == 1 ? sX1 : s == 2 ? sX2 : sX3; };
 
     const int N = a.N, K = a.K;
     int mt, nt;
@@ -136,6 +132,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
+    const int uwave = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform (SGPR) copy
+    const int l16 = lane & 15, lq = lane >> 4;
 
     // K-blocked operands: step kt of this tile is one contiguous block of
     // 256 rows x BK for the weights (stride N * BK between steps) and for the
@@ -146,144 +144,157 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
 
     // Lane l of load instruction q writes LDS bytes [q*1024 + l*16, +16): tile
     // row r = RPI*q + l/CH, stored chunk l%CH, which holds logical chunk
-    // (l%CH) ^ swz(r) of that row.
+    // (l%CH) ^ swz(r) of that row.  Token rows past the tile's end re-read its
+    // last row (never stored).
     int woff[QW], xoff[QX];
 #pragma unroll
     for (int i = 0; i < QW; ++i) {
         const int r = (wave * QW + i) * RPI + lane / CH;
-        woff[i] = (r * BK + (((lane % CH) ^ swz<CH>(r)) * 8)) * (int)sizeof(T);  // bytes
+        woff[i] = (r * BK + (((lane % CH) ^ swz(r)) * 8)) * (int)sizeof(T);  // bytes
     }
 #pragma unroll
     for (int i = 0; i < QX; ++i) {
         const int r = (wave * QX + i) * RPI + lane / CH;
         const int rr = r < nrows ? r : nrows - 1;
-        xoff[i] = (rr * BK + (((lane % CH) ^ swz<CH>(r)) * 8)) * (int)sizeof(T);  // bytes
+        xoff[i] = (rr * BK + (((lane % CH) ^ swz(r)) * 8)) * (int)sizeof(T);  // bytes
     }
 
-    f32x16_t acc[SN][SM];
+    f32x4_t acc[SN][SM];
 #pragma unroll
     for (int i = 0; i < SN; ++i)
 #pragma unroll
         for (int j = 0; j < SM; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+            for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.0f;
 
-    const int uwave = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform (SGPR) copy
-    auto issue = [&](int kt, int buf) {
-        const T* ws = Wt + kt * wstep;
-        const T* xs = Xt + kt * xstep;
-        const uint32_t bw = lds_addr(stW(buf)) + uwave * QW * RPI * BK * (int)sizeof(T);
-        const uint32_t bx = lds_addr(stX(buf)) + uwave * QX * RPI * BK * (int)sizeof(T);
-#pragma unroll
-        for (int i = 0; i < QW; ++i)
-            lds_dma16(ws, woff[i], bw + i * RPI * BK * (int)sizeof(T));
-#pragma unroll
-        for (int i = 0; i < QX; ++i)
-            lds_dma16(xs, xoff[i], bx + i * RPI * BK * (int)sizeof(T));
-        // keep the loads ahead of the MFMAs that follow
-        __builtin_amdgcn_sched_barrier(0);
+    // load q (0..Q-1) of step kt into ring slot `slot`: q < QW are weight
+    // rows, the rest token rows
+    auto dma = [&](int q, int kt, int slot) {
+        if (q < QW)
+            lds_dma16(Wt + kt * wstep, woff[q],
+                      lds_addr(stW(slot)) + (uwave * QW + q) * RPI * BK * (int)sizeof(T));
+        else
+            lds_dma16(Xt + kt * xstep, xoff[q - QW],
+                      lds_addr(stX(slot)) + (uwave * QX + q - QW) * RPI * BK * (int)sizeof(T));
     };
-    const int l32 = lane & 31, lhi = lane >> 5;
-    // MFMAs of stage `buf`, with the Q loads of step `ktl` into stage `bufl`
-    // spread through them (one load per NMF / Q MFMAs): a burst of loads at
-    // the top of the stage would stall this wave's in-order issue while the
-    // memory pipeline drains, and with it the MFMAs behind them.
-    constexpr int NMF = (BK / 16) * SN * SM;
-    constexpr int EVERY = NMF / Q;
-    static_assert(NMF % Q == 0, "loads must divide the MFMA count");
-    auto compute_issue = [&](int buf, int ktl, int bufl) {
-        const T* cW = stW(buf);
-        const T* cX = stX(buf);
-        const T* ws = Wt + ktl * wstep;
-        const T* xs = Xt + ktl * xstep;
-        const uint32_t bw = lds_addr(stW(bufl)) + uwave * QW * RPI * BK * (int)sizeof(T);
-        const uint32_t bx = lds_addr(stX(bufl)) + uwave * QX * RPI * BK * (int)sizeof(T);
-#pragma unroll
-        for (int ks = 0; ks < BK / 16; ++ks) {
-            const int kc = ks * 2 + lhi;
-            V av[SN], bv[SM];
-#pragma unroll
-            for (int i = 0; i < SN; ++i) {
-                const int r = wn * WN + i * 32 + l32;
-                av[i] = *reinterpret_cast<const V*>(&cW[r * BK + ((kc ^ swz<CH>(r)) * 8)]);
-            }
-#pragma unroll
-            for (int j = 0; j < SM; ++j) {
-                const int r = wm * WM + j * 32 + l32;
-                bv[j] = *reinterpret_cast<const V*>(&cX[r * BK + ((kc ^ swz<CH>(r)) * 8)]);
-            }
-#pragma unroll
-            for (int i = 0; i < SN; ++i) {
-#pragma unroll
-                for (int j = 0; j < SM; ++j) {
-                    const int m = (ks * SN + i) * SM + j;  // compile-time after unrolling
-                    if (m % EVERY == 0) {
-                        const int q = m / EVERY;
-                        if (q < QW) lds_dma16(ws, woff[q], bw + q * RPI * BK * (int)sizeof(T));
-                        else lds_dma16(xs, xoff[q - QW], bx + (q - QW) * RPI * BK * (int)sizeof(T));
-                    }
-                    acc[i][j] = Mfma<T>::run(av[i], bv[j], acc[i][j]);
-                }
-            }
-        }
+    // operand fragments: lane (l16, lq) holds row l16 of a 16-row block, k chunk lq
+    auto rdA = [&](int slot, int i) -> V {
+        const int r = wn * WN + i * 16 + l16;
+        return *reinterpret_cast<const V*>(&stW(slot)[r * BK + ((lq ^ swz(r)) * 8)]);
+    };
+    auto rdB = [&](int slot, int j) -> V {
+        const int r = wm * WM + j * 16 + l16;
+        return *reinterpret_cast<const V*>(&stX(slot)[r * BK + ((lq ^ swz(r)) * 8)]);
     };
 
-    // K / BK is a multiple of S (checked by the launcher).  Step kt computes
-    // stage kt % S.  Before it, the loads of stages <= kt must have landed:
-    // this wave's by vmcnt (exactly S - 2 later stages stay in flight), every
-    // wave's by the barrier.  The barrier also frees stage (kt - 1) % S, which
-    // is refilled with step kt + S - 1.  Past the end the last step is loaded
-    // again into that freed (never again read) stage, which keeps the loop
-    // free of branches and the in-flight count constant.  A bare s_barrier is
-    // used: __syncthreads() would add a full vmcnt(0) fence.
+    // Stage s (ring slot s % 4) runs the 64 MFMAs of k step s as 8 rows
+    // (weight block i) of 8 (token block j), with one block barrier B_s in the
+    // middle:
+    //   rows 0..3  read A block 4+i of stage s (used 4 rows later) and issue
+    //              loads 4..7 of step s + 2 (into slot (s + 2) % 4, which
+    //              every wave finished reading before B_{s-1});
+    //   B_s        this wave's loads of step s + 1 have landed (exactly the 8
+    //              loads of step s + 2 may still be in flight); after the
+    //              barrier every wave's have, and every wave is done with
+    //              stage s - 1;
+    //   rows 4..7  read A block i-4 of stage s + 1 into the register that
+    //              row i-4 freed, and issue loads 0..3 of step s + 3 (into
+    //              slot (s - 1) % 4);
+    //   row 7      after MFMA (7, j), read B block j of stage s + 1 into the
+    //              register that MFMA was the last to use (8 MFMAs ahead).
+    // Every fragment read thus lands well ahead of its MFMA with only 16
+    // fragment registers, and each load is pinned right behind an MFMA: a
+    // load can stall this wave's in-order issue while the memory pipeline is
+    // busy, and behind a fresh MFMA that stall overlaps the MFMA instead of
+    // idling the matrix core.  Loads past the end re-load the last step (into
+    // slots that are never read again), which keeps the loop branch-free and
+    // the wait counts constant.
     const int KT = K / BK;
+    auto cl = [&](int kt) { return kt < KT ? kt : KT - 1; };
+    // Bias slice first: wave 0's oldest load, so the first wait (step 0
+    // landed) also covers it.  Read only by the epilogue.
+    if (uwave == 0)
+        lds_dma16(a.bias + (int64_t)e * N + n0, lane * 16, lds_addr(sBias));
 #pragma unroll
-    for (int s = 0; s < S - 1; ++s) issue(s, s);
+    for (int q = 0; q < Q; ++q) dma(q, 0, 0);
+#pragma unroll
+    for (int q = 0; q < Q; ++q) dma(q, cl(1), 1);
+#pragma unroll
+    for (int q = 0; q < Q / 2; ++q) dma(q, cl(2), 2);
+    wait_vmcnt<Q + Q / 2>();
+    __builtin_amdgcn_s_barrier();  // bare: __syncthreads() would add a vmcnt(0) fence
+    __builtin_amdgcn_sched_barrier(0);
+    V fa[SN], fb[SM];
+#pragma unroll
+    for (int j = 0; j < SM; ++j) fb[j] = rdB(0, j);
+#pragma unroll
+    for (int i = 0; i < SN / 2; ++i) fa[i] = rdA(0, i);
+    __builtin_amdgcn_sched_barrier(0);
     for (int kt0 = 0; kt0 < KT; kt0 += S) {
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-            const int kt = kt0 + s;
-            wait_vmcnt<(S - 2) * Q>();
-            __builtin_amdgcn_s_barrier();
-            __builtin_amdgcn_sched_barrier(0);
-            compute_issue(s, min(kt + S - 1, KT - 1), (s + S - 1) % S);
+        for (int u = 0; u < S; ++u) {
+            const int s = kt0 + u;
+#pragma unroll
+            for (int i = 0; i < SN; ++i) {
+                if (i == SN / 2) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    wait_vmcnt<Q>();
+                    __builtin_amdgcn_s_barrier();
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                if (i < SN / 2) fa[SN / 2 + i] = rdA(u, SN / 2 + i);
+                else fa[i - SN / 2] = rdA((u + 1) % S, i - SN / 2);
+#pragma unroll
+                for (int j = 0; j < SM; ++j) {
+                    acc[i][j] = Mfma<T>::run(fa[i], fb[j], acc[i][j]);
+                    if (i == SN - 1) fb[j] = rdB((u + 1) % S, j);
+                    if (j == 1) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (i < SN / 2) dma(Q / 2 + i, cl(s + 2), (u + 2) % S);
+                        else dma(i - SN / 2, cl(s + 3), (u + 3) % S);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+            }
         }
     }
     // drain the trailing loads before this block's LDS can be handed on
     wait_vmcnt<0>();
 
-    // Epilogue.  Lane (l32, lhi) of block (i, j) holds token row
-    // wm*WM + j*32 + l32 and weight rows wn*WN + i*32 + 8*(r/4) + 4*lhi + r%4.
-    const float* bias = a.bias + (int64_t)e * N;
+    // Epilogue.  Lane (l16, lq) of block (i, j) holds token row
+    // wm*WM + j*16 + l16 and weight rows wn*WN + i*16 + 4*lq + (0..3).
+    const float* bias = sBias - n0;  // indexed by output column
     T* out = static_cast<T*>(a.out);
 #pragma unroll
     for (int j = 0; j < SM; ++j) {
-        const int m = wm * WM + j * 32 + l32;
+        const int m = wm * WM + j * 16 + l16;
         if (m >= nrows) continue;
         if (MODE == kGateUp) {
             // h is written K-blocked for the down GEMM: (row, c) at
             // ((c / 32) * a_cap + row) * 32 + c % 32
             T* hrow = out + (int64_t)(row0 + m) * kKBlock;
 #pragma unroll
-            for (int q = 0; q < SN / 2; ++q) {
-                const int pbase = n0 + wn * WN + q * 64;  // packed row of gate unit 0 of the pair
+            for (int p = 0; p < SN / 4; ++p) {
 #pragma unroll
-                for (int g4 = 0; g4 < 4; ++g4) {
-                    const int off = 8 * g4 + 4 * lhi;
-                    const float4 bg = *reinterpret_cast<const float4*>(bias + pbase + off);
-                    const float4 bu = *reinterpret_cast<const float4*>(bias + pbase + 32 + off);
+                for (int b = 0; b < 2; ++b) {
+                    // gate block 4p + b, its up block 4p + b + 2 (32-row interleave)
+                    const int prow = n0 + wn * WN + p * 64 + b * 16 + 4 * lq;
+                    const float4 bg = *reinterpret_cast<const float4*>(bias + prow);
+                    const float4 bu = *reinterpret_cast<const float4*>(bias + prow + 32);
                     const float bgv[4] = {bg.x, bg.y, bg.z, bg.w};
                     const float buv[4] = {bu.x, bu.y, bu.z, bu.w};
                     T hv[4];
 #pragma unroll
                     for (int s = 0; s < 4; ++s) {
-                        const float g = acc[2 * q][j][g4 * 4 + s] + bgv[s];
-                        const float u = acc[2 * q + 1][j][g4 * 4 + s] + buv[s];
-                        hv[s] = Elt<T>::from_f32(g / (1.0f + __expf(-g)) * u);
+                        const float g = acc[4 * p + b][j][s] + bgv[s];
+                        const float u = acc[4 * p + b + 2][j][s] + buv[s];
+                        // silu(g) * u; the reciprocal (1 ulp) is far inside the
+                        // 16-bit rounding of h
+                        hv[s] = Elt<T>::from_f32(g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u);
                     }
                     uint2 raw;
                     __builtin_memcpy(&raw, hv, 8);
-                    const int hc = pbase / 2 + off;  // 4 columns inside one 32-block
+                    const int hc = (n0 + wn * WN + p * 64) / 2 + b * 16 + 4 * lq;
                     *reinterpret_cast<uint2*>(hrow + (int64_t)(hc / kKBlock) * a.a_cap * kKBlock +
                                               hc % kKBlock) = raw;
                 }
@@ -292,20 +303,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
             T* orow = out + (int64_t)(row0 + m) * N;
 #pragma unroll
             for (int i = 0; i < SN; ++i) {
-                const int nb = n0 + wn * WN + i * 32;
+                const int nb = n0 + wn * WN + i * 16 + 4 * lq;
+                const float4 b = *reinterpret_cast<const float4*>(bias + nb);
+                const float bv4[4] = {b.x, b.y, b.z, b.w};
+                T ov[4];
 #pragma unroll
-                for (int g4 = 0; g4 < 4; ++g4) {
-                    const int off = 8 * g4 + 4 * lhi;
-                    const float4 b = *reinterpret_cast<const float4*>(bias + nb + off);
-                    const float bv4[4] = {b.x, b.y, b.z, b.w};
-                    T ov[4];
-#pragma unroll
-                    for (int s = 0; s < 4; ++s)
-                        ov[s] = Elt<T>::from_f32(acc[i][j][g4 * 4 + s] + bv4[s]);
-                    uint2 raw;
-                    __builtin_memcpy(&raw, ov, 8);
-                    *reinterpret_cast<uint2*>(orow + nb + off) = raw;
-                }
+                for (int s = 0; s < 4; ++s) ov[s] = Elt<T>::from_f32(acc[i][j][s] + bv4[s]);
+                uint2 raw;
+                __builtin_memcpy(&raw, ov, 8);
+                *reinterpret_cast<uint2*>(orow + nb) = raw;
             }
         }
     }
@@ -314,6 +320,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
 template <typename T, int MODE>
 hipError_t launch_mfma_t(const GemmArgs& a, hipStream_t s) {
     constexpr int BM = kMfmaBM, BN = kMfmaBN;
+    // whole column tiles, and whole turns of the ring in K
     if (a.N % BN != 0 || a.K % (kBK * kStages) != 0) return hipErrorInvalidValue;
     const int64_t grid = tile_grid(a.max_tiles, a.N / BN);
     if (grid <= 0) return hipSuccess;
