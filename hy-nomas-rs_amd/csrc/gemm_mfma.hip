@@ -89,6 +89,10 @@ __device__ __forceinline__ void lds_dma16(const void* sbase, uint32_t voff, uint
 }
 #pragma clang diagnostic pop
 
+// Word 3 of a raw buffer resource (gfx9 family: 32-bit data format, no
+// swizzle); with stride 0 the buffer is a plain byte range [0, num_records).
+constexpr int kBufferRsrcWord3 = 0x00020000;
+
 template <typename P>
 __device__ __forceinline__ uint32_t lds_addr(P* p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
@@ -121,9 +125,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
     auto stX = [&](int s) -> T* { return s == 0 ? sX0 : s == 1 ? sX1 : s == 2 ? sX2 : sX3; };
 
     const int N = a.N, K = a.K;
-    int mt, nt;
-    if (!tile_coords(blockIdx.x, N / BN, a.max_tiles, &mt, &nt)) return;
-    if (mt >= *a.tile_total) return;
+    const int KT_tile = K / BK;  // k steps of a whole tile
+    // live row tiles (the scan never lists more than max_tiles)
+    const int live = min(*a.tile_total, a.max_tiles);
+    WorkUnit wu;
+    if (!unit_coords(blockIdx.x, N / BN, live, KT_tile / S, &wu)) return;
+    const int mt = wu.mt, nt = wu.nt;
     const TileInfo ti = a.tiles[mt];
     const int e = ti.expert, row0 = ti.row0, nrows = ti.rows;
     if (e < 0 || e >= a.num_experts || nrows < 1 || row0 < 0 || row0 + (int64_t)nrows > a.a_cap)
@@ -138,9 +145,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
     // K-blocked operands: step kt of this tile is one contiguous block of
     // 256 rows x BK for the weights (stride N * BK between steps) and for the
     // token rows (stride a_cap * BK).
-    const T* Wt = static_cast<const T*>(a.W) + ((int64_t)e * (K / BK) * N + n0) * BK;
-    const T* Xt = static_cast<const T*>(a.X) + (int64_t)row0 * BK;
+    // A split unit walks its own 1/parts of the k steps.
+    const int KT = KT_tile / wu.parts;
     const int64_t wstep = (int64_t)N * BK, xstep = a.a_cap * BK;
+    const T* Wt = static_cast<const T*>(a.W) + ((int64_t)e * KT_tile * N + n0) * BK +
+                  (int64_t)wu.part * KT * wstep;
+    const T* Xt = static_cast<const T*>(a.X) + (int64_t)row0 * BK + (int64_t)wu.part * KT * xstep;
 
     // Lane l of load instruction q writes LDS bytes [q*1024 + l*16, +16): tile
     // row r = RPI*q + l/CH, stored chunk l%CH, which holds logical chunk
@@ -209,7 +219,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
     // idling the matrix core.  Loads past the end re-load the last step (into
     // slots that are never read again), which keeps the loop branch-free and
     // the wait counts constant.
-    const int KT = K / BK;
     auto cl = [&](int kt) { return kt < KT ? kt : KT - 1; };
     // Bias slice first: wave 0's oldest load, so the first wait (step 0
     // landed) also covers it.  Read only by the epilogue.
@@ -260,6 +269,58 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
     }
     // drain the trailing loads before this block's LDS can be handed on
     wait_vmcnt<0>();
+
+    if (wu.parts > 1) {
+        // Part of a split tile: publish the partial sums, count arrivals; the
+        // last part to arrive adds all parts in part order (the same order
+        // whichever part that is, so results do not depend on timing) and
+        // runs the epilogue.  Partials are written and read with agent-scope
+        // coherent accesses (sc1: through to the point of coherence of all
+        // XCDs), and every write has completed (vmcnt 0) before the counter
+        // moves, so no L2-wide write-back or invalidate is needed.  Reads past
+        // the tile's `parts` partials return zero (buffer range check).  The
+        // counter goes back to zero for the next launch.
+        constexpr int NB = SN * SM;
+        static_assert(NB * 4 * kThreads == kSplitUnitFloats, "one unit = one 256 x 256 tile");
+        constexpr int kUnitBytes = (int)(kSplitUnitFloats * sizeof(float));
+        constexpr int kSc1 = 16;  // cache policy: agent scope
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            a.split_ws + (int64_t)wu.slot * wu.parts * kSplitUnitFloats, 0, wu.parts * kUnitBytes,
+            kBufferRsrcWord3);
+#pragma unroll
+        for (int i = 0; i < SN; ++i)
+#pragma unroll
+            for (int j = 0; j < SM; ++j)
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    acc[i][j], rs, wu.part * kUnitBytes + ((i * SM + j) * kThreads + tid) * 16, 0, kSc1);
+        wait_vmcnt<0>();
+        __shared__ int s_last;
+        __syncthreads();
+        if (tid == 0) s_last = atomicAdd(&a.split_cnt[wu.slot], 1) == wu.parts - 1;
+        __syncthreads();
+        if (!s_last) return;
+        // one weight block at a time: its 8 x kMaxSplit loads all in flight
+        // before the first add
+#pragma unroll
+        for (int i = 0; i < SN; ++i) {
+            f32x4_t v[SM][kMaxSplit];
+#pragma unroll
+            for (int j = 0; j < SM; ++j)
+#pragma unroll
+                for (int p = 0; p < kMaxSplit; ++p)
+                    v[j][p] = __builtin_amdgcn_raw_buffer_load_b128(
+                        rs, p * kUnitBytes + ((i * SM + j) * kThreads + tid) * 16, 0, kSc1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < SM; ++j) {
+                f32x4_t t = v[j][0];
+#pragma unroll
+                for (int p = 1; p < kMaxSplit; ++p) t += v[j][p];
+                acc[i][j] = t;
+            }
+        }
+        if (tid == 0) a.split_cnt[wu.slot] = 0;
+    }
 
     // Epilogue.  Lane (l16, lq) of block (i, j) holds token row
     // wm*WM + j*16 + l16 and weight rows wn*WN + i*16 + 4*lq + (0..3).
@@ -322,8 +383,11 @@ hipError_t launch_mfma_t(const GemmArgs& a, hipStream_t s) {
     constexpr int BM = kMfmaBM, BN = kMfmaBN;
     // whole column tiles, and whole turns of the ring in K
     if (a.N % BN != 0 || a.K % (kBK * kStages) != 0) return hipErrorInvalidValue;
-    const int64_t grid = tile_grid(a.max_tiles, a.N / BN);
-    if (grid <= 0) return hipSuccess;
+    if (a.split_ws == nullptr || a.split_cnt == nullptr) return hipErrorInvalidValue;
+    // whole tiles, plus one round for the K-split units of a short last round
+    static_assert(kSplitUnits == kRound, "the split units fill one round");
+    const int64_t grid = tile_grid(a.max_tiles, a.N / BN) + kSplitUnits;
+    if (a.max_tiles <= 0) return hipSuccess;
     if (grid > 0x7fffffff) return hipErrorInvalidValue;
     hipLaunchKernelGGL((gemm_mfma_kernel<T, MODE, BM, BN, kBK, kStages>), dim3((unsigned)grid),
                        dim3(kThreads), 0, s, a);

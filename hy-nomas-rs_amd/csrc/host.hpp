@@ -127,6 +127,8 @@ private:
     void* d_xperm_ = nullptr;
     void* d_h_ = nullptr;
     void* d_yperm_ = nullptr;
+    float* d_split_ws_ = nullptr;     // MFMA path: partial tiles of K-split GEMM tails
+    int32_t* d_split_cnt_ = nullptr;  // their arrival counters
 
     int64_t last_rows_ = -1;
     hipStream_t last_stream_ = nullptr;

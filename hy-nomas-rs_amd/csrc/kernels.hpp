@@ -77,7 +77,15 @@ struct GemmArgs {
     int K;
     int num_experts;  // experts with weights (tiles naming others are skipped)
     int64_t a_cap;    // rows of X / out (tiles reaching beyond are skipped)
+    // MFMA path: f32 partial sums of tiles split along K (kSplitUnits units of
+    // kSplitUnitFloats each) and one arrival counter per split tile (zero
+    // between launches: the last part to arrive resets it)
+    float* split_ws;
+    int32_t* split_cnt;
 };
+// One split unit's partial tile: 256 x 256 f32.
+constexpr int64_t kSplitUnitFloats = 256 * 256;
+constexpr int kSplitUnits = 256;
 
 struct CombineArgs {
     const void* y_perm;

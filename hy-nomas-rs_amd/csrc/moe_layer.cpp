@@ -284,10 +284,18 @@ int MoeLayer::ensure_workspace(int64_t rows) {
     const size_t o_xp = take(es * A * D_);
     const size_t o_h = take(es * A * H_);
     const size_t o_yp = take(es * A * D_);
+    const size_t o_sw = mfma_ ? take(sizeof(float) * kSplitUnitFloats * kSplitUnits) : 0;
+    const size_t o_sc = mfma_ ? take(sizeof(int32_t) * kSplitUnits) : 0;
     free_workspace();
     void* ws = nullptr;
     HIP_TRY(hipMalloc(&ws, off));
     d_ws_ = ws;
+    if (mfma_) {
+        // the split-tile counters start at zero; the GEMMs keep them there.
+        // Finished before any stream (blocking or not) can use the workspace.
+        HIP_TRY(hipMemset(static_cast<uint8_t*>(ws) + o_sc, 0, sizeof(int32_t) * kSplitUnits));
+        HIP_TRY(hipDeviceSynchronize());
+    }
     uint8_t* b = static_cast<uint8_t*>(ws);
     d_idx_ = reinterpret_cast<int32_t*>(b + o_idx);
     d_w_ = reinterpret_cast<float*>(b + o_w);
@@ -302,6 +310,8 @@ int MoeLayer::ensure_workspace(int64_t rows) {
     d_xperm_ = b + o_xp;
     d_h_ = b + o_h;
     d_yperm_ = b + o_yp;
+    d_split_ws_ = mfma_ ? reinterpret_cast<float*>(b + o_sw) : nullptr;
+    d_split_cnt_ = mfma_ ? reinterpret_cast<int32_t*>(b + o_sc) : nullptr;
     cap_rows_ = cap;
     return NOMAS_OK;
 }
@@ -399,6 +409,8 @@ int MoeLayer::forward(const void* x, void* y, int64_t rows, hipStream_t s) {
     g1.K = (int)D_;
     g1.num_experts = (int)Ecols_;
     g1.a_cap = cap_rows_ * kslots_;
+    g1.split_ws = d_split_ws_;
+    g1.split_cnt = d_split_cnt_;
     STAGE(mfma_ ? launch_gemm_gate_up_mfma(dt_, g1, s) : launch_gemm_gate_up_simt(dt_, g1, s),
           "gate/up GEMM");
     if ((rc = mark(4))) return rc;

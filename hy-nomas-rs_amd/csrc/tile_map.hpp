@@ -1,4 +1,4 @@
-// Block-id -> GEMM tile mapping of the grouped MFMA GEMMs (host + device, so
+// Block-id -> GEMM work mapping of the grouped MFMA GEMMs (host + device, so
 // the mapping is checked exhaustively on the CPU).
 #pragma once
 
@@ -9,35 +9,96 @@ namespace nomas {
 constexpr int kTileGroupM = 8;   // row tiles per group (row index fastest inside)
 constexpr int kXcds = 8;         // MI355X: 8 XCDs
 constexpr int kCusPerXcd = 32;   // 32 CUs per XCD
+constexpr int kRound = kXcds * kCusPerXcd;  // blocks that run at once (one per CU)
+constexpr int kMaxSplit = 4;     // most parts a tail tile is split into along K
 
 // Grid size: the tile count padded to whole rounds of all XCDs.
 __host__ __device__ inline long long tile_grid(int max_tiles, int ntn) {
-    const long long pad = (long long)kXcds * kCusPerXcd;
-    return ((long long)max_tiles * ntn + pad - 1) / pad * pad;
+    return ((long long)max_tiles * ntn + kRound - 1) / kRound * kRound;
 }
 
-// Maps the hardware block id to (row tile mt, column tile nt); returns false
-// for padding blocks.  Blocks are dispatched in id order, block i to XCD
-// i % 8, so one XCD's queue is ids x, x+8, ...  Its k-th group of kCusPerXcd
-// consecutive queue entries ("round") runs roughly at time k.  Round
-// R = k * 8 + x takes logical tiles [R * kCusPerXcd, (R + 1) * kCusPerXcd):
-// at any time the eight XCDs work on eight consecutive rounds (the same
-// expert's weights, shared through the MALL), and inside an XCD a round is a
-// kTileGroupM x 8 block of tiles sharing panels in that XCD's L2.
-__host__ __device__ inline bool tile_coords(int pid, int ntn, int max_tiles, int* mt, int* nt) {
+// Blocks are dispatched in id order, block i to XCD i % 8, so one XCD's queue
+// is ids x, x+8, ...  Its k-th group of kCusPerXcd consecutive queue entries
+// ("round") runs roughly at time k.  Round R = k * 8 + x takes logical
+// indices [R * kCusPerXcd, (R + 1) * kCusPerXcd): logical order is time order,
+// and at any time the eight XCDs work on eight consecutive rounds.  A
+// bijection of [0, n) for every n that is a multiple of kRound.
+__host__ __device__ inline int time_order(int pid) {
     const int xcd = pid % kXcds, loc = pid / kXcds;
     const int round = (loc / kCusPerXcd) * kXcds + xcd;
-    const int L = round * kCusPerXcd + loc % kCusPerXcd;
-    // a partial last group holds only gm * ntn tiles: reject every index at
-    // or past max_tiles * ntn, not just whole groups
-    if (L >= max_tiles * ntn) return false;
-    const int group = L / (kTileGroupM * ntn);
-    const int first_m = group * kTileGroupM;
-    const int gm = max_tiles - first_m < kTileGroupM ? max_tiles - first_m : kTileGroupM;
-    const int within = L - group * kTileGroupM * ntn;
+    return round * kCusPerXcd + loc % kCusPerXcd;
+}
+
+// Tile (mt, nt) of logical index L < tiles * ntn: groups of kTileGroupM row
+// tiles x all column tiles, row index fastest inside a group.  Consecutive
+// rounds then share the same expert's weights (through the MALL), and a
+// round inside an XCD is an 8 x 4 block of tiles sharing panels in its L2.
+__host__ __device__ inline void group_tile(long long L, int ntn, int tiles, int* mt, int* nt) {
+    const long long group = L / ((long long)kTileGroupM * ntn);
+    const int first_m = (int)group * kTileGroupM;
+    const int gm = tiles - first_m < kTileGroupM ? tiles - first_m : kTileGroupM;
+    const int within = (int)(L - group * kTileGroupM * ntn);
     *mt = first_m + within % gm;
     *nt = within / gm;
+}
+
+// Maps the hardware block id to (row tile mt, column tile nt) of a grid of
+// max_tiles x ntn tiles; returns false for padding blocks.
+__host__ __device__ inline bool tile_coords(int pid, int ntn, int max_tiles, int* mt, int* nt) {
+    const int L = time_order(pid);
+    // a partial last group holds only gm * ntn tiles: reject every index at
+    // or past max_tiles * ntn, not just whole groups
+    if (L >= (long long)max_tiles * ntn) return false;
+    group_tile(L, ntn, max_tiles, mt, nt);
     return *nt < ntn;
+}
+
+// Parts the tiles of the last, partial round are split into along K, for T
+// live tiles and `turns` whole k-loop turns per tile: when that round would
+// keep at most half the CUs busy for a whole tile, its r tiles become
+// parts * r <= kRound shorter units.  Parts must divide the turns.
+__host__ __device__ inline int split_parts(long long T, int turns) {
+    const int r = (int)(T % kRound);
+    if (r == 0 || 2 * r > kRound) return 1;
+    int p = kMaxSplit;
+    while (p > 1 && (p * r > kRound || turns % p != 0)) p >>= 1;
+    return p;
+}
+
+// One block's work: a whole tile (parts == 1), or part `part` of `parts` of
+// a tile split along K; `slot` numbers the split tiles (0 .. r - 1).
+struct WorkUnit {
+    int mt, nt;
+    int part, parts;
+    int slot;
+};
+
+// Work of block pid when `tiles` row tiles are live (tiles <= the max_tiles
+// the grid was sized for, grid = tile_grid(max_tiles, ntn) + kRound).  Whole
+// tiles come first in time order; the split units of the last r tiles come
+// last and fill the final round.  Returns false for blocks with no work.
+__host__ __device__ inline bool unit_coords(int pid, int ntn, int tiles, int turns, WorkUnit* u) {
+    const long long T = (long long)tiles * ntn;
+    const long long L = time_order(pid);
+    const int parts = split_parts(T, turns);
+    const long long F = parts > 1 ? T - T % kRound : T;  // whole tiles
+    long long tile;
+    if (L < F) {
+        tile = L;
+        u->part = 0;
+        u->parts = 1;
+        u->slot = -1;
+    } else if (L < F + (T - F) * parts) {
+        const long long q = L - F;
+        tile = F + q / parts;
+        u->part = (int)(q % parts);
+        u->parts = parts;
+        u->slot = (int)(q / parts);
+    } else {
+        return false;
+    }
+    group_tile(tile, ntn, tiles, &u->mt, &u->nt);
+    return true;
 }
 
 }  // namespace nomas

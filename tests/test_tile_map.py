@@ -1,9 +1,13 @@
-"""The GEMM block -> tile mapping (csrc/tile_map.hpp), checked exhaustively on the CPU.
+"""The GEMM block -> work mapping (csrc/tile_map.hpp), checked exhaustively on the CPU.
 
 The same header is compiled into the gfx950 kernels; here it is compiled for
 the host.  For every (row tiles, column tiles) pair in a broad range, every
 block of the padded grid either is rejected as padding or names a tile in
-range, and every tile is named exactly once.
+range, and every tile is named exactly once.  For the work units (whole
+tiles, plus the K-split parts of a short last round) every live tile is
+covered exactly once, or by exactly `parts` distinct parts that share one
+workspace slot; split units come after every whole tile in time order and
+fill at most one round.
 """
 import os
 import shutil
@@ -38,13 +42,48 @@ int main() {
         if (hit[i] != 1) { printf("tile %lld named %d times (%d, %d)\n", i, hit[i], max_tiles, ntn); return 1; }
       ++pairs;
     }
-  printf("ok %ld\n", pairs);
+  // work units
+  const int turns_set[] = {1, 2, 3, 6, 12, 24, 64};
+  long units_checked = 0;
+  for (int max_tiles = 1; max_tiles <= 150; ++max_tiles)
+    for (int tiles = 0; tiles <= max_tiles; tiles += (max_tiles > 40 ? 7 : 1))
+      for (int ntn = 1; ntn <= 66; ntn += (tiles > 60 ? 5 : 1))
+        for (int turns : turns_set) {
+          const long long T = (long long)tiles * ntn;
+          const long long grid = nomas::tile_grid(max_tiles, ntn) + nomas::kRound;
+          std::vector<int> whole(T, 0), parts_seen(T, 0), slot_of(T, -1), pmask(T, 0), npart(T, 0);
+          std::vector<int> slot_used(nomas::kRound, 0);
+          long long last_whole = -1, first_split = 1LL << 60;
+          for (long long pid = 0; pid < grid; ++pid) {
+            nomas::WorkUnit u;
+            if (!nomas::unit_coords((int)pid, ntn, tiles, turns, &u)) continue;
+            if (u.mt < 0 || u.mt >= tiles || u.nt < 0 || u.nt >= ntn) { printf("unit out of range\n"); return 1; }
+            const long long t = (long long)u.mt * ntn + u.nt, L = nomas::time_order((int)pid);
+            if (u.parts == 1) { whole[t]++; if (L > last_whole) last_whole = L; continue; }
+            if (u.parts < 2 || u.parts > nomas::kMaxSplit || turns % u.parts || u.part < 0 || u.part >= u.parts ||
+                u.slot < 0 || u.slot * u.parts >= nomas::kRound) { printf("bad split unit\n"); return 1; }
+            if (slot_of[t] != -1 && slot_of[t] != u.slot) { printf("slot mismatch\n"); return 1; }
+            slot_of[t] = u.slot; npart[t] = u.parts;
+            if (pmask[t] & (1 << u.part)) { printf("part twice\n"); return 1; }
+            pmask[t] |= 1 << u.part; parts_seen[t]++;
+            if (L < first_split) first_split = L;
+          }
+          for (long long t = 0; t < T; ++t) {
+            const bool ok = (whole[t] == 1 && parts_seen[t] == 0) ||
+                            (whole[t] == 0 && parts_seen[t] == npart[t] && pmask[t] == (1 << npart[t]) - 1);
+            if (!ok) { printf("tile %lld covered wrongly (%d, %d, %d)\n", t, tiles, ntn, turns); return 1; }
+            if (slot_of[t] >= 0) { if (slot_used[slot_of[t]]++) { printf("slot shared\n"); return 1; } }
+          }
+          if (first_split < (1LL << 60) && first_split < last_whole) { printf("split before whole\n"); return 1; }
+          ++units_checked;
+        }
+  printf("ok %ld %ld\n", pairs, units_checked);
   return 0;
 }
 """
 
 
-def test_tile_mapping_is_a_bijection_onto_valid_tiles(tmp_path):
+def test_tile_and_work_unit_mappings(tmp_path):
     hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(hipcc):
         pytest.skip("hipcc not available")
