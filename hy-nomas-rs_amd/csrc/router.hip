@@ -1,17 +1,18 @@
 // Router: logits = x . Wr^T, softmax, top-k and renormalised gates, fused in
 // one kernel (hy-nomas-rs moe.rs:67-95).
 //
-// One block = 8 waves = one chunk of 64 rows; each wave routes 8 rows, as two
-// passes of 4 rows over x.
-//  - Logits accumulate in f64.  Every product of two bf16/f16 inputs is exact
-//    in f32 and of two f32 inputs in the f64 fma, so the only rounding is the
-//    f64 sum: indices are then
-//    decided far below the 1e-6 logit near-tie threshold.  The kernel reads
-//    x once (T*D*b bytes): HBM-bound.
-//  - Lanes split D in 16-byte chunks; each lane keeps 4 rows x 8 experts of
-//    partial sums, then a butterfly reduce-scatter (5 halving xor-shuffle
-//    steps + 1 full step: 32 shuffles instead of 32*6) leaves every sum on one
-//    lane pair.
+// One block = 16 waves = one chunk of 64 rows.
+//  - Logits are f64 matrix products (v_mfma_f64_16x16x4_f64).  A product of
+//    two bf16/f16 or two f32 inputs is exact in f64, so the only rounding is
+//    the f64 summation (relative 1e-16): expert choice is decided far below
+//    the 1e-6 logit near-tie threshold, as by an exact evaluation.
+//  - Wave (g, q) computes rows 16g..16g+15 of the chunk against 16 experts at
+//    a time over the q-th quarter of D; the four quarters are added in a fixed
+//    order (q = 0, 1, 2, 3) through LDS, so results do not depend on timing.
+//    Each lane loads 16 contiguous bytes of its row (and of its expert's
+//    weights) per step and feeds them to consecutive MFMAs: the k index of
+//    MFMA i, lane group lg is k0 + lg * EPC + i, the same assignment for both
+//    operands, so the 4-deep MFMA k dimension reads whole 16-byte chunks.
 //  - Selection is wave-parallel over experts: max / sum / k rounds of argmax
 //    are xor-shuffle reductions across the wave.  Ties go to the lowest
 //    expert index, the reference's first-max-wins argmax (moe.rs:78-80).
@@ -22,16 +23,21 @@
 //    (block level) the chunk's per-expert histogram for the dispatch scan.
 //    With a shared dense branch the row gets one more slot: expert E with
 //    gate `dense_coef` (moe.rs:103-106 adds it after the experts).
+//  The kernel reads x once (T*D*b bytes) and the router weights from L2.
 #include "kernels.hpp"
 
 namespace nomas {
 
 namespace {
 
-constexpr int kRouterThreads = 512;  // 8 waves; each routes 8 rows as 2 passes of 4
-constexpr int kRowsPerPass = 4;
+constexpr int kRouterThreads = 1024;  // 16 waves
+constexpr int kGroups = 4;            // row groups of 16 rows
+constexpr int kParts = 4;             // quarters of D
 constexpr int kRowsPerWave = kRouterRows / (kRouterThreads / kWave);
-constexpr int kExpGroup = 8;
+static_assert(kGroups * 16 == kRouterRows, "4 groups of 16 rows per chunk");
+static_assert(kGroups * kParts * kWave == kRouterThreads, "one wave per (group, part)");
+
+typedef double d4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ double wave_max(double v) {
 #pragma unroll
@@ -45,12 +51,10 @@ __device__ __forceinline__ double wave_sum(double v) {
     return v;
 }
 
-// acc + x * w with the product exact: a product of two 16-bit floats fits the
-// 24-bit f32 significand, two f32 need the f64 fma.
-template <typename T>
-__device__ __forceinline__ double acc_exact(float x, float w, double acc) {
-    if constexpr (sizeof(T) == 2) return acc + (double)(x * w);
-    else return __builtin_fma((double)x, (double)w, acc);
+// LDS layout (bytes): logits [64][E] f64, parts 1..3 of the current 16-expert
+// block [3][4 groups][16][16] f64, counts [E + 1] int.
+__host__ __device__ inline size_t router_lds(int E) {
+    return sizeof(double) * ((size_t)kRouterRows * E + 3 * kGroups * 256) + sizeof(int) * (E + 1);
 }
 
 template <typename T>
@@ -58,74 +62,83 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
     const T* __restrict__ x, const T* __restrict__ wr, int64_t rows, int D, int E, int k,
     int k_slots, float dense_coef, int32_t* __restrict__ topk_idx, float* __restrict__ topk_w,
     float* __restrict__ gap, int32_t* __restrict__ chunk_counts) {
-    extern __shared__ double s_logit[];  // [kRouterRows][E]
-    int* s_cnt = reinterpret_cast<int*>(s_logit + kRouterRows * E);  // [E + 1]
+    extern __shared__ double s_logit[];                                   // [kRouterRows][E]
+    double* s_part = s_logit + kRouterRows * E;                           // [3][kGroups][16][16]
+    int* s_cnt = reinterpret_cast<int*>(s_part + 3 * kGroups * 256);      // [E + 1]
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int E_cols = E + (k_slots > k ? 1 : 0);
     for (int e = tid; e < E_cols; e += kRouterThreads) s_cnt[e] = 0;
 
-    constexpr int EPC = 16 / sizeof(T);
-    const int nchunk = D / EPC;
+    constexpr int EPC = 16 / sizeof(T);  // elements per 16-byte chunk = MFMAs per step
+    constexpr int CK = 4 * EPC;          // k per step (4 lane groups)
     const int64_t chunk_row0 = (int64_t)blockIdx.x * kRouterRows;
+    const int g = wave / kParts, q = wave % kParts;
+    const int r16 = lane & 15, lg = lane >> 4;
+    const int64_t row = chunk_row0 + g * 16 + r16;
+    const bool row_ok = row < rows;
+    const T* xr = x + (row_ok ? row : 0) * (int64_t)D;
+    // this part's steps: a contiguous quarter of them
+    const int nstep = (D + CK - 1) / CK;
+    const int s0 = (int)((int64_t)nstep * q / kParts), s1 = (int)((int64_t)nstep * (q + 1) / kParts);
 
-    for (int pass = 0; pass < kRowsPerWave / kRowsPerPass; ++pass) {
-        const int lr0 = wave * kRowsPerWave + pass * kRowsPerPass;
-        bool valid[kRowsPerPass];
-        const T* xr[kRowsPerPass];
+    // Loads run kPre steps ahead of the MFMAs (a ring of raw 16-byte chunks
+    // in registers), so the memory latency of x is paid once per pipeline
+    // fill, not once per step.
+    constexpr int kPre = 4;
+    auto unpack = [](const uint4& raw, int i) -> double {
+        Vec16<T> t;
+        __builtin_memcpy(&t, &raw, 16);
+        return (double)Elt<T>::to_f32(t.v[i]);
+    };
+    for (int e0 = 0; e0 < E; e0 += 16) {
+        const int ex = e0 + r16;
+        const bool ex_ok = ex < E;
+        const T* wrr = wr + (int64_t)(ex_ok ? ex : 0) * D;
+        auto fetch = [&](int st, uint4& xa, uint4& wa) {
+            const int kk = st * CK + lg * EPC;  // D % 8 == 0: a chunk is wholly in or out
+            const uint4 z = make_uint4(0, 0, 0, 0);
+            xa = (st < s1 && row_ok && kk < D) ? *reinterpret_cast<const uint4*>(xr + kk) : z;
+            wa = (st < s1 && ex_ok && kk < D) ? *reinterpret_cast<const uint4*>(wrr + kk) : z;
+        };
+        uint4 xb[kPre], wb[kPre];
 #pragma unroll
-        for (int r = 0; r < kRowsPerPass; ++r) {
-            const int64_t row = chunk_row0 + lr0 + r;
-            valid[r] = row < rows;
-            xr[r] = x + (valid[r] ? row : 0) * (int64_t)D;
+        for (int p = 0; p < kPre; ++p) fetch(s0 + p, xb[p], wb[p]);
+        d4 c0 = {0.0, 0.0, 0.0, 0.0}, c1 = {0.0, 0.0, 0.0, 0.0};
+        // whole turns of the ring: steps past s1 hold zeros, which add exactly 0
+        for (int st0 = s0; st0 < s1; st0 += kPre) {
+#pragma unroll
+            for (int p = 0; p < kPre; ++p) {
+#pragma unroll
+                for (int i = 0; i < EPC; ++i) {
+                    const double xd = unpack(xb[p], i), wd = unpack(wb[p], i);
+                    if (i & 1) c1 = __builtin_amdgcn_mfma_f64_16x16x4f64(xd, wd, c1, 0, 0, 0);
+                    else c0 = __builtin_amdgcn_mfma_f64_16x16x4f64(xd, wd, c0, 0, 0, 0);
+                }
+                fetch(st0 + p + kPre, xb[p], wb[p]);
+            }
         }
-        if (!valid[0]) break;  // wave-uniform: no row of this pass exists
-        for (int e0 = 0; e0 < E; e0 += kExpGroup) {
-            double v[kRowsPerPass * kExpGroup];  // partial sums, index r * kExpGroup + g
+        const d4 c = c0 + c1;
+        // lane holds rows lg + 4 r (r = 0..3) of the group, expert column r16;
+        // part 0 writes the logit slots, parts 1..3 their own buffers
+        __syncthreads();  // the previous block's reads of s_part are done
 #pragma unroll
-            for (int i = 0; i < kRowsPerPass * kExpGroup; ++i) v[i] = 0.0;
-            for (int c = lane; c < nchunk; c += kWave) {
-                float xv[kRowsPerPass][EPC];
-#pragma unroll
-                for (int r = 0; r < kRowsPerPass; ++r) {
-                    if (valid[r]) {
-                        load16(xr[r] + (int64_t)c * EPC, xv[r]);
-                    } else {
-#pragma unroll
-                        for (int i = 0; i < EPC; ++i) xv[r][i] = 0.0f;
-                    }
-                }
-#pragma unroll
-                for (int g = 0; g < kExpGroup; ++g) {
-                    if (e0 + g < E) {
-                        float wv[EPC];
-                        load16(wr + (int64_t)(e0 + g) * D + (int64_t)c * EPC, wv);
-#pragma unroll
-                        for (int i = 0; i < EPC; ++i)
-#pragma unroll
-                            for (int r = 0; r < kRowsPerPass; ++r)
-                                v[r * kExpGroup + g] = acc_exact<T>(xv[r][i], wv[i], v[r * kExpGroup + g]);
-                    }
-                }
+        for (int r = 0; r < 4; ++r) {
+            const int i = lg + 4 * r;
+            if (q == 0) {
+                if (ex_ok) s_logit[(g * 16 + i) * E + ex] = c[r];
+            } else {
+                s_part[((q - 1) * kGroups + g) * 256 + i * 16 + r16] = c[r];
             }
-            // Butterfly reduce-scatter of the 32 partial sums over the 64 lanes.
+        }
+        __syncthreads();
+        // logit = ((p0 + p1) + p2) + p3
+        {
+            const int gg = tid >> 8, i = (tid >> 4) & 15, j = tid & 15;
+            if (e0 + j < E) {
+                double v = s_logit[(gg * 16 + i) * E + e0 + j];
 #pragma unroll
-            for (int step = 0; step < 5; ++step) {
-                const int o = 32 >> step;
-                const int half = 16 >> step;
-                const bool upper = (lane & o) != 0;
-#pragma unroll
-                for (int i = 0; i < half; ++i) {
-                    const double send = upper ? v[i] : v[i + half];
-                    const double keep = upper ? v[i + half] : v[i];
-                    v[i] = keep + __shfl_xor(send, o);
-                }
-            }
-            v[0] += __shfl_xor(v[0], 1);
-            // Lane l now holds the full sum of value index (l >> 1) & 31.
-            if ((lane & 1) == 0) {
-                const int vi = (lane >> 1) & 31;
-                const int r = vi / kExpGroup, g = vi % kExpGroup;
-                if (e0 + g < E) s_logit[(lr0 + r) * E + e0 + g] = v[0];
+                for (int p = 0; p < kParts - 1; ++p) v += s_part[(p * kGroups + gg) * 256 + i * 16 + j];
+                s_logit[(gg * 16 + i) * E + e0 + j] = v;
             }
         }
     }
@@ -134,19 +147,19 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
     const int per_lane = (E + kWave - 1) / kWave;  // experts per lane (<= 4 for E <= 256)
     for (int r = 0; r < kRowsPerWave; ++r) {
         const int lr = wave * kRowsPerWave + r;
-        const int64_t row = chunk_row0 + lr;
-        if (row >= rows) break;  // wave-uniform
-        const double* lg = s_logit + lr * E;
+        const int64_t orow = chunk_row0 + lr;
+        if (orow >= rows) break;  // wave-uniform
+        const double* lgt = s_logit + lr * E;
         double m = -INFINITY;
         for (int j = 0; j < per_lane; ++j) {
             const int e = lane + j * kWave;
-            if (e < E) m = fmax(m, lg[e]);
+            if (e < E) m = fmax(m, lgt[e]);
         }
         m = wave_max(m);
         double s = 0.0;
         for (int j = 0; j < per_lane; ++j) {
             const int e = lane + j * kWave;
-            if (e < E) s += exp(lg[e] - m);
+            if (e < E) s += exp(lgt[e] - m);
         }
         s = wave_sum(s);
 
@@ -158,7 +171,7 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
             for (int j = 0; j < per_lane; ++j) {
                 const int e = lane + j * kWave;
                 if (e < E && !((sel >> j) & 1u)) {
-                    const double lv = lg[e];
+                    const double lv = lgt[e];
                     if (bi < 0 || lv > bv) { bv = lv; bi = e; }
                 }
             }
@@ -175,8 +188,8 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
         for (int j = 0; j < per_lane; ++j) {
             const int e = lane + j * kWave;
             if (e >= E) continue;
-            if ((sel >> j) & 1u) psel += exp(lg[e] - m) / s;
-            else best_un = fmax(best_un, lg[e]);
+            if ((sel >> j) & 1u) psel += exp(lgt[e] - m) / s;
+            else best_un = fmax(best_un, lgt[e]);
         }
         best_un = wave_max(best_un);
         psel = wave_sum(psel);
@@ -188,18 +201,18 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
             if (is_sel) {
                 const int e = lane + j * kWave;
                 const int rank = base + __popcll(bal & ((1ull << lane) - 1ull));
-                const double p = exp(lg[e] - m) / s;
-                topk_idx[row * k_slots + rank] = e;
-                topk_w[row * k_slots + rank] = (float)(p / (psel + 1e-9));
+                const double p = exp(lgt[e] - m) / s;
+                topk_idx[orow * k_slots + rank] = e;
+                topk_w[orow * k_slots + rank] = (float)(p / (psel + 1e-9));
                 atomicAdd(&s_cnt[e], 1);
             }
             base += __popcll(bal);
         }
         if (lane == 0) {
-            gap[row] = (k == E) ? INFINITY : (float)(kth - best_un);
+            gap[orow] = (k == E) ? INFINITY : (float)(kth - best_un);
             if (k_slots > k) {
-                topk_idx[row * k_slots + k] = E;
-                topk_w[row * k_slots + k] = dense_coef;
+                topk_idx[orow * k_slots + k] = E;
+                topk_w[orow * k_slots + k] = dense_coef;
                 atomicAdd(&s_cnt[E], 1);
             }
         }
@@ -212,7 +225,8 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
 template <typename T>
 hipError_t launch_router_t(const RouterArgs& a, hipStream_t s) {
     const int nblk = (int)((a.rows + kRouterRows - 1) / kRouterRows);
-    const size_t lds = sizeof(double) * kRouterRows * a.E + sizeof(int) * (a.E + 1);
+    if (nblk == 0) return hipSuccess;
+    const size_t lds = router_lds(a.E);
     if (lds > 65536) {
         hipError_t err = hipFuncSetAttribute((const void*)router_kernel<T>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -226,7 +240,7 @@ hipError_t launch_router_t(const RouterArgs& a, hipStream_t s) {
 
 }  // namespace
 
-size_t router_lds_bytes(int E) { return sizeof(double) * kRouterRows * E + sizeof(int) * (E + 1); }
+size_t router_lds_bytes(int E) { return router_lds(E); }
 
 hipError_t launch_router(DType dt, const RouterArgs& a, hipStream_t s) {
     switch (dt) {
