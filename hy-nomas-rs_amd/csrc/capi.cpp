@@ -54,6 +54,85 @@ LinF32 random_lin(uint64_t seed, const std::string& path, int64_t in_f, int64_t 
     return l;
 }
 
+// One Lin to read from a checkpoint: `key`.weight (out_f, in_f) and, with
+// `bias`, `key`.bias (out_f,).
+struct Want {
+    std::string key;
+    int64_t out_f, in_f;
+    bool bias;
+};
+
+// Lin::load over the named files (weights.rs:105-145): every wanted tensor
+// must be present (missing keys are one error listing the first few in sorted
+// order, weights.rs:117-127) and have the wanted shape.
+int load_lins(const char* const* files, int64_t n_files, const std::vector<Want>& want,
+              std::vector<LinF32>* lins) {
+    std::vector<std::string> names;
+    for (const Want& w : want) {
+        names.push_back(w.key + ".weight");
+        if (w.bias) names.push_back(w.key + ".bias");
+    }
+    std::vector<std::string> fl;
+    for (int64_t i = 0; i < n_files; ++i) {
+        if (!files[i]) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "files[%lld] is null", (long long)i);
+        fl.emplace_back(files[i]);
+    }
+    std::map<std::string, nomas::StTensor> ts;
+    int rc = nomas::read_safetensors(fl, names, &ts);
+    if (rc != NOMAS_OK) return rc;
+    std::vector<std::string> missing;
+    for (const std::string& n : names)
+        if (!ts.count(n)) missing.push_back(n);
+    std::sort(missing.begin(), missing.end());
+    if (!missing.empty()) {
+        std::string list;
+        for (size_t i = 0; i < missing.size() && i < 5; ++i) list += (i ? ", " : "") + missing[i];
+        return set_error(NOMAS_ERR_WEIGHT_KEY, "checkpoint is missing %zu model keys, first few: [%s]",
+                         missing.size(), list.c_str());
+    }
+    lins->assign(want.size(), LinF32());
+    for (size_t i = 0; i < want.size(); ++i) {
+        const Want& w = want[i];
+        LinF32* l = &(*lins)[i];
+        const nomas::StTensor& tw = ts[w.key + ".weight"];
+        if (tw.shape.size() != 2 || tw.shape[0] != w.out_f || tw.shape[1] != w.in_f)
+            return set_error(NOMAS_ERR_WEIGHT_KEY, "%s.weight: expected shape (%lld, %lld)",
+                             w.key.c_str(), (long long)w.out_f, (long long)w.in_f);
+        rc = nomas::st_to_f32(tw, &l->w);
+        if (rc != NOMAS_OK) return rc;
+        if (w.bias) {
+            const nomas::StTensor& tb = ts[w.key + ".bias"];
+            if (tb.shape.size() != 1 || tb.shape[0] != w.out_f)
+                return set_error(NOMAS_ERR_WEIGHT_KEY, "%s.bias: expected shape (%lld,)",
+                                 w.key.c_str(), (long long)w.out_f);
+            rc = nomas::st_to_f32(tb, &l->b);
+            if (rc != NOMAS_OK) return rc;
+        }
+    }
+    return NOMAS_OK;
+}
+
+// The dense feed-forward is checked like a one-expert MoE.
+const nomas_moe_config kDenseCfg = {1, 1, 0.0, 0};
+
+int make_dense(int64_t dim, int64_t hidden, int dtype, int device, std::unique_ptr<MoeLayer>* out) {
+    int rc = MoeLayer::check_shape(kDenseCfg, dim, hidden, dtype);
+    if (rc != NOMAS_OK) return rc;
+    int ndev = 0;
+    hipError_t e = hipGetDeviceCount(&ndev);
+    if (e != hipSuccess || ndev <= 0)
+        return set_error(NOMAS_ERR_HIP, "no HIP device available (%s)",
+                         e == hipSuccess ? "0 devices" : hipGetErrorString(e));
+    if (device < 0 || device >= ndev)
+        return set_error(NOMAS_ERR_INVALID_ARGUMENT, "device %d out of range (%d devices)", device, ndev);
+    try {
+        out->reset(new MoeLayer(MoeLayer::DenseTag{}, dim, hidden, static_cast<DType>(dtype), device));
+    } catch (const std::bad_alloc&) {
+        return set_error(NOMAS_ERR_OUT_OF_MEMORY, "host allocation failed");
+    }
+    return NOMAS_OK;
+}
+
 int finish(std::unique_ptr<MoeLayer> layer, nomas_moe_t** out) {
     try {
         *out = new nomas_moe{std::move(layer)};
@@ -118,7 +197,6 @@ int nomas_moe_from_safetensors(const nomas_moe_config* cfg, const char* const* f
     if (rc != NOMAS_OK) return rc;
     const std::string base(path);
     const bool dense = cfg->shared_dense > 0.0;
-    struct Want { std::string key; int64_t out_f, in_f; bool bias; };
     std::vector<Want> want;
     want.push_back({base + ".router", cfg->experts, dim, false});
     for (int64_t e = 0; e < cfg->experts; ++e) {
@@ -132,66 +210,24 @@ int nomas_moe_from_safetensors(const nomas_moe_config* cfg, const char* const* f
         want.push_back({base + ".dense.up", hidden, dim, true});
         want.push_back({base + ".dense.down", dim, hidden, true});
     }
-    std::vector<std::string> names;
-    for (const Want& w : want) {
-        names.push_back(w.key + ".weight");
-        if (w.bias) names.push_back(w.key + ".bias");
-    }
-    std::vector<std::string> fl;
-    for (int64_t i = 0; i < n_files; ++i) {
-        if (!files[i]) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "files[%lld] is null", (long long)i);
-        fl.emplace_back(files[i]);
-    }
-    std::map<std::string, nomas::StTensor> ts;
-    rc = nomas::read_safetensors(fl, names, &ts);
+    std::vector<LinF32> lins;
+    rc = load_lins(files, n_files, want, &lins);
     if (rc != NOMAS_OK) return rc;
-    // Missing keys are an error, listing the first few in sorted order
-    // (weights.rs:117-127).
-    std::vector<std::string> missing;
-    for (const std::string& n : names)
-        if (!ts.count(n)) missing.push_back(n);
-    std::sort(missing.begin(), missing.end());
-    if (!missing.empty()) {
-        std::string list;
-        for (size_t i = 0; i < missing.size() && i < 5; ++i) list += (i ? ", " : "") + missing[i];
-        return set_error(NOMAS_ERR_WEIGHT_KEY, "checkpoint is missing %zu model keys, first few: [%s]",
-                         missing.size(), list.c_str());
-    }
-    auto get = [&](const Want& w, LinF32* l) -> int {
-        const nomas::StTensor& tw = ts[w.key + ".weight"];
-        if (tw.shape.size() != 2 || tw.shape[0] != w.out_f || tw.shape[1] != w.in_f)
-            return set_error(NOMAS_ERR_WEIGHT_KEY, "%s.weight: expected shape (%lld, %lld)",
-                             w.key.c_str(), (long long)w.out_f, (long long)w.in_f);
-        int r = nomas::st_to_f32(tw, &l->w);
-        if (r != NOMAS_OK) return r;
-        if (w.bias) {
-            const nomas::StTensor& tb = ts[w.key + ".bias"];
-            if (tb.shape.size() != 1 || tb.shape[0] != w.out_f)
-                return set_error(NOMAS_ERR_WEIGHT_KEY, "%s.bias: expected shape (%lld,)",
-                                 w.key.c_str(), (long long)w.out_f);
-            r = nomas::st_to_f32(tb, &l->b);
-            if (r != NOMAS_OK) return r;
-        }
-        return NOMAS_OK;
-    };
     MoeParamsF32 p;
     size_t wi = 0;
-    if ((rc = get(want[wi++], &p.router))) return rc;
-    p.gate.resize(cfg->experts);
-    p.up.resize(cfg->experts);
-    p.down.resize(cfg->experts);
+    p.router = std::move(lins[wi++]);
     for (int64_t e = 0; e < cfg->experts; ++e) {
-        if ((rc = get(want[wi++], &p.gate[e]))) return rc;
-        if ((rc = get(want[wi++], &p.up[e]))) return rc;
-        if ((rc = get(want[wi++], &p.down[e]))) return rc;
+        p.gate.push_back(std::move(lins[wi++]));
+        p.up.push_back(std::move(lins[wi++]));
+        p.down.push_back(std::move(lins[wi++]));
     }
     if (dense) {
         p.has_dense = true;
-        if ((rc = get(want[wi++], &p.dgate))) return rc;
-        if ((rc = get(want[wi++], &p.dup))) return rc;
-        if ((rc = get(want[wi++], &p.ddown))) return rc;
+        p.dgate = std::move(lins[wi++]);
+        p.dup = std::move(lins[wi++]);
+        p.ddown = std::move(lins[wi++]);
     }
-    ts.clear();
+    lins.clear();
     std::unique_ptr<MoeLayer> layer;
     rc = make_layer(cfg, dim, hidden, dtype, device, &layer);
     if (rc != NOMAS_OK) return rc;
@@ -271,6 +307,121 @@ int nomas_moe_stage_times(nomas_moe_t* h, float* ms6) {
 int nomas_moe_uses_mfma(const nomas_moe_t* h) { return h && h->layer->uses_mfma() ? 1 : 0; }
 
 void nomas_moe_destroy(nomas_moe_t* h) { delete h; }
+
+// ---- dense SwiGLU feed-forward (mlp.rs:9-59) ----------------------------------
+
+struct nomas_ffn {
+    std::unique_ptr<MoeLayer> layer;
+};
+
+static int finish_ffn(std::unique_ptr<MoeLayer> layer, nomas_ffn_t** out) {
+    try {
+        *out = new nomas_ffn{std::move(layer)};
+    } catch (const std::bad_alloc&) {
+        return set_error(NOMAS_ERR_OUT_OF_MEMORY, "host allocation failed");
+    }
+    return NOMAS_OK;
+}
+
+int nomas_ffn_from_random(const char* path, int64_t dim, int64_t hidden, int dtype, uint64_t seed,
+                          int device, nomas_ffn_t** out) {
+    nomas::clear_error();
+    if (!path || !out) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    std::unique_ptr<MoeLayer> layer;
+    int rc = make_dense(dim, hidden, dtype, device, &layer);
+    if (rc != NOMAS_OK) return rc;
+    MoeParamsF32 p;
+    const std::string base(path);
+    try {
+        p.gate.push_back(random_lin(seed, base + ".gate", dim, hidden, true));
+        p.up.push_back(random_lin(seed, base + ".up", dim, hidden, true));
+        p.down.push_back(random_lin(seed, base + ".down", hidden, dim, true));
+    } catch (const std::bad_alloc&) {
+        return set_error(NOMAS_ERR_OUT_OF_MEMORY, "host allocation failed");
+    }
+    rc = layer->upload_f32(p);
+    if (rc != NOMAS_OK) return rc;
+    return finish_ffn(std::move(layer), out);
+}
+
+int nomas_ffn_from_safetensors(const char* const* files, int64_t n_files, const char* path,
+                               int64_t dim, int64_t hidden, int dtype, int device,
+                               nomas_ffn_t** out) {
+    nomas::clear_error();
+    if (!files || n_files < 1 || !path || !out)
+        return set_error(NOMAS_ERR_INVALID_ARGUMENT, "null argument or no files");
+    *out = nullptr;
+    int rc = MoeLayer::check_shape(kDenseCfg, dim, hidden, dtype);
+    if (rc != NOMAS_OK) return rc;
+    const std::string base(path);
+    const std::vector<Want> want = {{base + ".gate", hidden, dim, true},
+                                    {base + ".up", hidden, dim, true},
+                                    {base + ".down", dim, hidden, true}};
+    std::vector<LinF32> lins;
+    rc = load_lins(files, n_files, want, &lins);
+    if (rc != NOMAS_OK) return rc;
+    MoeParamsF32 p;
+    p.gate.push_back(std::move(lins[0]));
+    p.up.push_back(std::move(lins[1]));
+    p.down.push_back(std::move(lins[2]));
+    lins.clear();
+    std::unique_ptr<MoeLayer> layer;
+    rc = make_dense(dim, hidden, dtype, device, &layer);
+    if (rc != NOMAS_OK) return rc;
+    rc = layer->upload_f32(p);
+    if (rc != NOMAS_OK) return rc;
+    return finish_ffn(std::move(layer), out);
+}
+
+int nomas_ffn_from_host(int64_t dim, int64_t hidden, int dtype, int device, const void* gate_w,
+                        const void* gate_b, const void* up_w, const void* up_b, const void* down_w,
+                        const void* down_b, nomas_ffn_t** out) {
+    nomas::clear_error();
+    if (!out) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    if (!gate_w || !up_w || !down_w)
+        return set_error(NOMAS_ERR_INVALID_ARGUMENT, "gate/up/down weights must be non-null");
+    int rc = MoeLayer::check_shape(kDenseCfg, dim, hidden, dtype);
+    if (rc != NOMAS_OK) return rc;
+    std::unique_ptr<MoeLayer> layer;
+    rc = make_dense(dim, hidden, dtype, device, &layer);
+    if (rc != NOMAS_OK) return rc;
+    rc = layer->upload(nullptr, gate_w, gate_b, up_w, up_b, down_w, down_b, nullptr, nullptr,
+                       nullptr, nullptr, nullptr, nullptr);
+    if (rc != NOMAS_OK) return rc;
+    return finish_ffn(std::move(layer), out);
+}
+
+int nomas_ffn_forward(nomas_ffn_t* h, const void* x, void* y, int64_t rows, void* stream) {
+    nomas::clear_error();
+    if (!h) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "null handle");
+    return h->layer->forward(x, y, rows, static_cast<hipStream_t>(stream));
+}
+
+int nomas_ffn_forward_host(nomas_ffn_t* h, const void* x, void* y, int64_t rows) {
+    nomas::clear_error();
+    if (!h) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "null handle");
+    return h->layer->forward_host(x, y, rows);
+}
+
+int64_t nomas_ffn_n_params(const nomas_ffn_t* h) { return h ? h->layer->n_params() : -1; }
+
+int nomas_ffn_set_profiling(nomas_ffn_t* h, int enable) {
+    nomas::clear_error();
+    if (!h) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "null handle");
+    return h->layer->set_profiling(enable != 0);
+}
+
+int nomas_ffn_stage_times(nomas_ffn_t* h, float* ms6) {
+    nomas::clear_error();
+    if (!h) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "null handle");
+    return h->layer->stage_times(ms6);
+}
+
+int nomas_ffn_uses_mfma(const nomas_ffn_t* h) { return h && h->layer->uses_mfma() ? 1 : 0; }
+
+void nomas_ffn_destroy(nomas_ffn_t* h) { delete h; }
 
 const char* nomas_moe_last_error(void) { return nomas::last_error(); }
 

@@ -7,6 +7,8 @@
 // ascending row order (a stable permutation), so every run produces the same
 // buffers, and combine sums a row's slots in ascending expert order, the order
 // of the reference's accumulation loop (moe.rs:98-102).
+#include <algorithm>
+
 #include "kernels.hpp"
 
 namespace nomas {
@@ -210,6 +212,38 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     }
 }
 
+// Dense feed-forward: every row goes to expert 0, in order.
+__global__ void dense_tiles_kernel(int64_t rows, int BM, int max_tiles, TileInfo* tiles,
+                                   int32_t* tile_total) {
+    const int64_t ntiles = (rows + BM - 1) / BM;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < max_tiles; i += gridDim.x * blockDim.x) {
+        TileInfo t;
+        t.expert = 0;
+        t.row0 = i * BM;
+        t.rows = i < ntiles ? (int)min<int64_t>(BM, rows - (int64_t)i * BM) : 0;
+        t.pad = 0;
+        tiles[i] = t;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) *tile_total = (int32_t)min<int64_t>(ntiles, max_tiles);
+}
+
+// x (rows x D, row-major) to the K-blocked layout of the MFMA GEMMs: one
+// 16-byte chunk per thread, coalesced reads, 64-byte runs written.
+template <typename T>
+__global__ __launch_bounds__(256) void kblock_kernel(const T* __restrict__ x, T* __restrict__ xk,
+                                                     int64_t rows, int D, int64_t a_cap) {
+    constexpr int EPC = 16 / sizeof(T);
+    const int nchunk = D / EPC;
+    const int64_t total = rows * nchunk;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / nchunk;
+        const int64_t col = (i % nchunk) * EPC;
+        const uint4 v = *reinterpret_cast<const uint4*>(x + r * D + col);
+        *reinterpret_cast<uint4*>(xk + ((col / kKBlock) * a_cap + r) * kKBlock + col % kKBlock) = v;
+    }
+}
+
 template <typename T>
 hipError_t launch_dispatch_t(const DispatchArgs& a, hipStream_t s) {
     const int nblk = (int)((a.rows + kRouterRows - 1) / kRouterRows);
@@ -244,6 +278,35 @@ hipError_t launch_dispatch(DType dt, const DispatchArgs& a, hipStream_t s) {
         case DType::F16: return launch_dispatch_t<_Float16>(a, s);
     }
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_dense_tiles(int64_t rows, int BM, int max_tiles, TileInfo* tiles,
+                              int32_t* tile_total, hipStream_t s) {
+    if (max_tiles <= 0) return hipErrorInvalidValue;
+    const int nblk = (max_tiles + 255) / 256;
+    hipLaunchKernelGGL(dense_tiles_kernel, dim3(nblk), dim3(256), 0, s, rows, BM, max_tiles, tiles,
+                       tile_total);
+    return hipGetLastError();
+}
+
+hipError_t launch_kblock(DType dt, const void* x, void* xk, int64_t rows, int D, int64_t a_cap,
+                         hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    if (D % kKBlock != 0 || a_cap < rows) return hipErrorInvalidValue;
+    const int64_t chunks = rows * (D / (16 / (int)dtype_size(dt)));
+    const unsigned nblk = (unsigned)std::min<int64_t>((chunks + 255) / 256, 65536);
+    switch (dt) {
+        case DType::BF16:
+            hipLaunchKernelGGL(kblock_kernel<__bf16>, dim3(nblk), dim3(256), 0, s,
+                               (const __bf16*)x, (__bf16*)xk, rows, D, a_cap);
+            break;
+        case DType::F16:
+            hipLaunchKernelGGL(kblock_kernel<_Float16>, dim3(nblk), dim3(256), 0, s,
+                               (const _Float16*)x, (_Float16*)xk, rows, D, a_cap);
+            break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_combine(DType dt, const CombineArgs& a, hipStream_t s) {

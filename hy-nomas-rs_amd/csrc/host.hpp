@@ -61,6 +61,11 @@ struct MoeParamsF32 {
 class MoeLayer {
 public:
     MoeLayer(const nomas_moe_config& cfg, int64_t dim, int64_t hidden, DType dt, int device);
+    // A dense SwiGLU feed-forward (mlp.rs:39-48): one expert that every row
+    // goes to with gate 1, no router; forward skips routing, dispatch and
+    // combine.
+    struct DenseTag {};
+    MoeLayer(DenseTag, int64_t dim, int64_t hidden, DType dt, int device);
     ~MoeLayer();
     MoeLayer(const MoeLayer&) = delete;
     MoeLayer& operator=(const MoeLayer&) = delete;
@@ -90,6 +95,7 @@ public:
     int64_t top_k() const { return k_; }
     DType dtype() const { return dt_; }
     bool uses_mfma() const { return mfma_; }
+    bool dense_only() const { return dense_only_; }
 
 private:
     int ensure_workspace(int64_t rows);
@@ -103,6 +109,8 @@ private:
     int device_;
     bool mfma_;
     int BM_;
+    bool dense_only_ = false;
+    int forward_dense(const void* x, void* y, int64_t rows, hipStream_t s);
 
     // device weights
     void* d_wr_ = nullptr;

@@ -109,5 +109,12 @@ hipError_t launch_gemm_down_mfma(DType dt, const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_gate_up_simt(DType dt, const GemmArgs& a, hipStream_t s);
 hipError_t launch_gemm_down_simt(DType dt, const GemmArgs& a, hipStream_t s);
 hipError_t launch_combine(DType dt, const CombineArgs& a, hipStream_t s);
+// Dense feed-forward (no routing): the tile table of `rows` rows of one
+// expert in BM-row tiles (max_tiles entries written), and x re-laid out
+// K-blocked ((col / 32) * a_cap + row) * 32 + col % 32 for the MFMA GEMM.
+hipError_t launch_dense_tiles(int64_t rows, int BM, int max_tiles, TileInfo* tiles,
+                              int32_t* tile_total, hipStream_t s);
+hipError_t launch_kblock(DType dt, const void* x, void* xk, int64_t rows, int D, int64_t a_cap,
+                         hipStream_t s);
 
 }  // namespace nomas

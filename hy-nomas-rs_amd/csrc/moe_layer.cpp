@@ -91,6 +91,15 @@ MoeLayer::MoeLayer(const nomas_moe_config& cfg, int64_t dim, int64_t hidden, DTy
     BM_ = mfma_ ? kMfmaBM : kSimtBM;
 }
 
+MoeLayer::MoeLayer(DenseTag, int64_t dim, int64_t hidden, DType dt, int device)
+    : D_(dim), H_(hidden), E_(1), k_(1), shared_dense_(0.0), dt_(dt), device_(device) {
+    Ecols_ = 1;
+    kslots_ = 1;
+    dense_only_ = true;
+    mfma_ = dt_ != DType::F32 && D_ % kMfmaBN == 0 && H_ % (kMfmaBN / 2) == 0;
+    BM_ = mfma_ ? kMfmaBM : kSimtBM;
+}
+
 MoeLayer::~MoeLayer() {
     DeviceGuard g(device_);
     free_workspace();
@@ -101,15 +110,18 @@ MoeLayer::~MoeLayer() {
 }
 
 int64_t MoeLayer::n_params() const {
-    // router (no bias) + experts (gate, up, down with biases); dense excluded (moe.rs:112-114).
-    return E_ * D_ + E_ * (2 * (H_ * D_ + H_) + (D_ * H_ + D_));
+    // gate, up, down with biases (mlp.rs:50-58)
+    const int64_t ffn = 2 * (H_ * D_ + H_) + (D_ * H_ + D_);
+    if (dense_only_) return ffn;
+    // router (no bias) + experts; dense excluded (moe.rs:112-114).
+    return E_ * D_ + E_ * ffn;
 }
 
 int MoeLayer::upload(const void* router_w, const void* gate_w, const void* gate_b,
                      const void* up_w, const void* up_b, const void* down_w, const void* down_b,
                      const void* dg_w, const void* dg_b, const void* du_w, const void* du_b,
                      const void* dd_w, const void* dd_b) {
-    if (!router_w || !gate_w || !up_w || !down_w)
+    if ((!router_w && !dense_only_) || !gate_w || !up_w || !down_w)
         return set_error(NOMAS_ERR_INVALID_ARGUMENT, "router/gate/up/down weights must be non-null");
     const bool dense = Ecols_ > E_;
     if (dense && (!dg_w || !du_w || !dd_w))
@@ -189,12 +201,12 @@ int MoeLayer::upload(const void* router_w, const void* gate_w, const void* gate_
         if (p) (void)hipFree(p);
     d_wr_ = d_w1_ = d_w2_ = nullptr;
     d_b1_ = d_b2_ = nullptr;
-    HIP_TRY(hipMalloc(&d_wr_, (size_t)(E_ * D) * es));
+    if (!dense_only_) HIP_TRY(hipMalloc(&d_wr_, (size_t)(E_ * D) * es));
     HIP_TRY(hipMalloc(&d_w1_, w1.size()));
     HIP_TRY(hipMalloc((void**)&d_b1_, b1.size() * sizeof(float)));
     HIP_TRY(hipMalloc(&d_w2_, w2.size()));
     HIP_TRY(hipMalloc((void**)&d_b2_, b2.size() * sizeof(float)));
-    HIP_TRY(hipMemcpy(d_wr_, router_w, (size_t)(E_ * D) * es, hipMemcpyHostToDevice));
+    if (!dense_only_) HIP_TRY(hipMemcpy(d_wr_, router_w, (size_t)(E_ * D) * es, hipMemcpyHostToDevice));
     HIP_TRY(hipMemcpy(d_w1_, w1.data(), w1.size(), hipMemcpyHostToDevice));
     HIP_TRY(hipMemcpy(d_b1_, b1.data(), b1.size() * sizeof(float), hipMemcpyHostToDevice));
     HIP_TRY(hipMemcpy(d_w2_, w2.data(), w2.size(), hipMemcpyHostToDevice));
@@ -226,7 +238,7 @@ int MoeLayer::upload_f32(const MoeParamsF32& p) {
     };
     const int64_t D = D_, H = H_;
     std::vector<uint8_t> r, gw, gb, uw, ub, dw, db, xgw, xgb, xuw, xub, xdw, xdb;
-    cvt(p.router.w, &r);
+    if (!dense_only_) cvt(p.router.w, &r);
     cvt(cat(p.gate, false, H * D), &gw);
     cvt(cat(p.gate, true, H), &gb);
     cvt(cat(p.up, false, H * D), &uw);
@@ -242,7 +254,7 @@ int MoeLayer::upload_f32(const MoeParamsF32& p) {
         cvt(p.ddown.w, &xdw);
         cvt(p.ddown.b.empty() ? std::vector<float>(D, 0.0f) : p.ddown.b, &xdb);
     }
-    return upload(r.data(), gw.data(), gb.data(), uw.data(), ub.data(), dw.data(), db.data(),
+    return upload(dense_only_ ? nullptr : r.data(), gw.data(), gb.data(), uw.data(), ub.data(), dw.data(), db.data(),
                   dense ? xgw.data() : nullptr, dense ? xgb.data() : nullptr,
                   dense ? xuw.data() : nullptr, dense ? xub.data() : nullptr,
                   dense ? xdw.data() : nullptr, dense ? xdb.data() : nullptr);
@@ -283,7 +295,7 @@ int MoeLayer::ensure_workspace(int64_t rows) {
     const size_t o_tt = take(sizeof(int32_t));
     const size_t o_xp = take(es * A * D_);
     const size_t o_h = take(es * A * H_);
-    const size_t o_yp = take(es * A * D_);
+    const size_t o_yp = dense_only_ ? 0 : take(es * A * D_);  // dense: the down GEMM writes y
     const size_t o_sw = mfma_ ? take(sizeof(float) * kSplitUnitFloats * kSplitUnits) : 0;
     const size_t o_sc = mfma_ ? take(sizeof(int32_t) * kSplitUnits) : 0;
     free_workspace();
@@ -309,7 +321,7 @@ int MoeLayer::ensure_workspace(int64_t rows) {
     d_tile_total_ = reinterpret_cast<int32_t*>(b + o_tt);
     d_xperm_ = b + o_xp;
     d_h_ = b + o_h;
-    d_yperm_ = b + o_yp;
+    d_yperm_ = dense_only_ ? nullptr : b + o_yp;
     d_split_ws_ = mfma_ ? reinterpret_cast<float*>(b + o_sw) : nullptr;
     d_split_cnt_ = mfma_ ? reinterpret_cast<int32_t*>(b + o_sc) : nullptr;
     cap_rows_ = cap;
@@ -332,6 +344,7 @@ int MoeLayer::forward(const void* x, void* y, int64_t rows, hipStream_t s) {
     int rc = ensure_workspace(rows);
     if (rc != NOMAS_OK) return rc;
     if (done_recorded_ && s != last_stream_) HIP_TRY(hipStreamWaitEvent(s, done_, 0));
+    if (dense_only_) return forward_dense(x, y, rows, s);
 
     const int nch = (int)((rows + kRouterRows - 1) / kRouterRows);
     const int mt = max_tiles(rows);
@@ -446,6 +459,75 @@ int MoeLayer::forward(const void* x, void* y, int64_t rows, hipStream_t s) {
     return NOMAS_OK;
 }
 
+// Dense feed-forward: the stages of the routed forward that remain.  Stage
+// slots for profiling: router (none), scan = tile table, dispatch = K-blocked
+// copy of x (MFMA path only), gate/up, down (written straight into y), combine
+// (none).
+int MoeLayer::forward_dense(const void* x, void* y, int64_t rows, hipStream_t s) {
+    int rc;
+    const int mt = max_tiles(rows);
+    hipEvent_t* ev = nullptr;
+    if (profiling_) {
+        ev = &events_[(size_t)(recorded_ % kRing) * 7];
+        ++recorded_;
+    }
+    auto mark = [&](int i) -> int {
+        if (ev) HIP_TRY(hipEventRecord(ev[i], s));
+        return NOMAS_OK;
+    };
+#define STAGE(call, what)                                                                  \
+    do {                                                                                   \
+        hipError_t _e = (call);                                                            \
+        if (_e != hipSuccess)                                                              \
+            return set_error(NOMAS_ERR_HIP, "%s launch failed: %s", what, hipGetErrorString(_e)); \
+    } while (0)
+    if ((rc = mark(0))) return rc;
+    if ((rc = mark(1))) return rc;
+    STAGE(launch_dense_tiles(rows, BM_, mt, d_tiles_, d_tile_total_, s), "tile table");
+    if ((rc = mark(2))) return rc;
+    // the MFMA GEMMs read K-blocked rows; the general path reads x in place
+    if (mfma_) STAGE(launch_kblock(dt_, x, d_xperm_, rows, (int)D_, cap_rows_, s), "K-blocked copy");
+    if ((rc = mark(3))) return rc;
+
+    GemmArgs g1;
+    g1.X = mfma_ ? d_xperm_ : x;
+    g1.W = d_w1_;
+    g1.bias = d_b1_;
+    g1.out = d_h_;
+    g1.tiles = d_tiles_;
+    g1.tile_total = d_tile_total_;
+    g1.max_tiles = mt;
+    g1.N = (int)(2 * H_);
+    g1.K = (int)D_;
+    g1.num_experts = 1;
+    // MFMA: the K-blocked buffers' row capacity; general: rows of x (row-major)
+    g1.a_cap = mfma_ ? cap_rows_ : rows;
+    g1.split_ws = d_split_ws_;
+    g1.split_cnt = d_split_cnt_;
+    STAGE(mfma_ ? launch_gemm_gate_up_mfma(dt_, g1, s) : launch_gemm_gate_up_simt(dt_, g1, s),
+          "gate/up GEMM");
+    if ((rc = mark(4))) return rc;
+
+    GemmArgs g2 = g1;
+    g2.X = d_h_;
+    g2.W = d_w2_;
+    g2.bias = d_b2_;
+    g2.out = y;  // rows stay in order: the output is y itself
+    g2.N = (int)D_;
+    g2.K = (int)H_;
+    STAGE(mfma_ ? launch_gemm_down_mfma(dt_, g2, s) : launch_gemm_down_simt(dt_, g2, s),
+          "down GEMM");
+    if ((rc = mark(5))) return rc;
+    if ((rc = mark(6))) return rc;
+#undef STAGE
+    if (!done_) HIP_TRY(hipEventCreateWithFlags(&done_, hipEventDisableTiming));
+    HIP_TRY(hipEventRecord(done_, s));
+    done_recorded_ = true;
+    last_rows_ = rows;
+    last_stream_ = s;
+    return NOMAS_OK;
+}
+
 int MoeLayer::forward_host(const void* x, void* y, int64_t rows) {
     if (rows < 0) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "rows must be >= 0");
     if (rows == 0) { last_rows_ = 0; return NOMAS_OK; }
@@ -474,6 +556,7 @@ int MoeLayer::forward_host(const void* x, void* y, int64_t rows) {
 }
 
 int MoeLayer::routing(int32_t* idx, float* w, int32_t* counts, float* gap) {
+    if (dense_only_) return set_error(NOMAS_ERR_STATE, "a dense feed-forward has no routing");
     if (last_rows_ < 0) return set_error(NOMAS_ERR_STATE, "no forward has run on this handle");
     DeviceGuard g(device_);
     HIP_TRY(hipStreamSynchronize(last_stream_));

@@ -26,8 +26,8 @@ from . import _lib
 from ._lib import nomas_moe_config
 
 __all__ = [
-    "DataType", "MoeConfig", "Weights", "MoeLayer", "NomasError", "InvalidConfig", "WeightKey",
-    "IoError", "path_seed", "randn_affine", "to_model_dtype",
+    "DataType", "MoeConfig", "Weights", "MoeLayer", "FeedForward", "NomasError", "InvalidConfig",
+    "WeightKey", "IoError", "path_seed", "randn_affine", "to_model_dtype",
 ]
 
 
@@ -308,6 +308,104 @@ class MoeLayer:
     def close(self) -> None:
         if self._h:
             _lib.lib().nomas_moe_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class FeedForward:
+    """Dense SwiGLU feed-forward (FeedForward::SwiGlu, mlp.rs:9-59) on one MI355X:
+    y = down(silu(gate(x)) * up(x)), on the expert GEMM kernels without routing."""
+
+    STAGES = ("router", "tile_table", "kblock_copy", "gemm_gate_up", "gemm_down", "combine")
+
+    def __init__(self, handle: C.c_void_p, dim: int, hidden: int, dtype: DataType, device: int):
+        self._h = handle
+        self.dim, self.hidden = int(dim), int(hidden)
+        self.dtype = dtype
+        self.device = device
+
+    # -- FeedForward::from_source (mlp.rs:18-37), Activation::Silu -------------
+    @classmethod
+    def from_source(cls, src: Weights, path: str, dim: int, hidden: int) -> "FeedForward":
+        L = _lib.lib()
+        h = C.c_void_p()
+        if src.kind == "random":
+            rc = L.nomas_ffn_from_random(path.encode(), dim, hidden, int(src.dtype),
+                                         src.seed & 0xFFFFFFFFFFFFFFFF, src.device, C.byref(h))
+        elif src.kind == "loaded":
+            arr = (C.c_char_p * len(src.files))(*[f.encode() for f in src.files])
+            rc = L.nomas_ffn_from_safetensors(arr, len(src.files), path.encode(), dim, hidden,
+                                              int(src.dtype), src.device, C.byref(h))
+        elif src.kind == "tensors":
+            t = src.tensors
+            D, H = int(dim), int(hidden)
+
+            def one(key, shape, required):
+                if key not in t:
+                    if required:
+                        raise WeightKey(3, f"missing tensor {key}")
+                    return None
+                a = np.asarray(t[key], np.float32)
+                if a.shape != shape:
+                    raise WeightKey(3, f"{key}: expected shape {shape}, got {a.shape}")
+                return to_model_dtype(a, src.dtype)
+
+            keep = [one(f"{path}.gate.weight", (H, D), True), one(f"{path}.gate.bias", (H,), False),
+                    one(f"{path}.up.weight", (H, D), True), one(f"{path}.up.bias", (H,), False),
+                    one(f"{path}.down.weight", (D, H), True), one(f"{path}.down.bias", (D,), False)]
+            ptrs = [None if a is None else a.ctypes.data for a in keep]
+            rc = L.nomas_ffn_from_host(D, H, int(src.dtype), src.device, *ptrs, C.byref(h))
+        else:
+            raise ValueError(f"unknown weight source {src.kind!r}")
+        _check(rc)
+        return cls(h, dim, hidden, src.dtype, src.device)
+
+    # -- FeedForward::forward (mlp.rs:39-48) -----------------------------------
+    def forward(self, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        """x: (..., D) in the model dtype, on the layer's GPU or on the host."""
+        if x.dim() < 1 or x.shape[-1] != self.dim:
+            raise NomasError(2, f"expected last dim {self.dim}, got shape {tuple(x.shape)}")
+        if x.dtype != self.dtype.torch:
+            raise NomasError(2, f"expected dtype {self.dtype.torch}, got {x.dtype}")
+        xc = x.contiguous()
+        rows = xc.numel() // self.dim
+        if out is None:
+            out = torch.empty_like(xc)
+        L = _lib.lib()
+        if xc.is_cuda:
+            stream = torch.cuda.current_stream(xc.device).cuda_stream
+            _check(L.nomas_ffn_forward(self._h, xc.data_ptr(), out.data_ptr(), rows, stream))
+        else:
+            _check(L.nomas_ffn_forward_host(self._h, xc.data_ptr(), out.data_ptr(), rows))
+        return out
+
+    __call__ = forward
+
+    def n_params(self) -> int:
+        """mlp.rs:50-58."""
+        return int(_lib.lib().nomas_ffn_n_params(self._h))
+
+    def set_profiling(self, on: bool) -> None:
+        _check(_lib.lib().nomas_ffn_set_profiling(self._h, 1 if on else 0))
+
+    def stage_times(self) -> dict:
+        """Average per-stage milliseconds of the forwards profiled since the last call."""
+        ms = (C.c_float * 6)()
+        _check(_lib.lib().nomas_ffn_stage_times(self._h, ms))
+        return dict(zip(self.STAGES, [float(v) for v in ms]))
+
+    @property
+    def uses_mfma(self) -> bool:
+        return bool(_lib.lib().nomas_ffn_uses_mfma(self._h))
+
+    def close(self) -> None:
+        if self._h:
+            _lib.lib().nomas_ffn_destroy(self._h)
             self._h = None
 
     def __del__(self):

@@ -67,6 +67,27 @@ def lib() -> C.CDLL:
     L.nomas_moe_uses_mfma.restype = i32
     L.nomas_moe_destroy.argtypes = [vp]
     L.nomas_moe_destroy.restype = None
+    L.nomas_ffn_from_random.argtypes = [C.c_char_p, i64, i64, i32, C.c_uint64, i32, hp]
+    L.nomas_ffn_from_random.restype = i32
+    L.nomas_ffn_from_safetensors.argtypes = [C.POINTER(C.c_char_p), i64, C.c_char_p, i64, i64, i32,
+                                             i32, hp]
+    L.nomas_ffn_from_safetensors.restype = i32
+    L.nomas_ffn_from_host.argtypes = [i64, i64, i32, i32] + [vp] * 6 + [hp]
+    L.nomas_ffn_from_host.restype = i32
+    L.nomas_ffn_forward.argtypes = [vp, vp, vp, i64, vp]
+    L.nomas_ffn_forward.restype = i32
+    L.nomas_ffn_forward_host.argtypes = [vp, vp, vp, i64]
+    L.nomas_ffn_forward_host.restype = i32
+    L.nomas_ffn_n_params.argtypes = [vp]
+    L.nomas_ffn_n_params.restype = i64
+    L.nomas_ffn_set_profiling.argtypes = [vp, i32]
+    L.nomas_ffn_set_profiling.restype = i32
+    L.nomas_ffn_stage_times.argtypes = [vp, vp]
+    L.nomas_ffn_stage_times.restype = i32
+    L.nomas_ffn_uses_mfma.argtypes = [vp]
+    L.nomas_ffn_uses_mfma.restype = i32
+    L.nomas_ffn_destroy.argtypes = [vp]
+    L.nomas_ffn_destroy.restype = None
     L.nomas_moe_last_error.argtypes = []
     L.nomas_moe_last_error.restype = C.c_char_p
     L.nomas_path_seed.argtypes = [C.c_uint64, C.c_char_p]

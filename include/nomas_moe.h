@@ -127,6 +127,51 @@ int nomas_moe_uses_mfma(const nomas_moe_t *h);
 
 void nomas_moe_destroy(nomas_moe_t *h);
 
+/* ---- Dense SwiGLU feed-forward ------------------------------------------------
+ * FeedForward::SwiGlu (nomas-core/src/modules/mlp.rs:9-59), the FFN of the DiT
+ * blocks when the config has no MoE (BlockFfn::Dense, block.rs:14-19,47-53):
+ * y = down(silu(gate(x)) * up(x)) with biases.  It runs on the same grouped
+ * GEMM kernels as the experts (one expert, no routing); the MoE conventions
+ * above apply (errors, dtypes, row folding, stream ordering). */
+typedef struct nomas_ffn nomas_ffn_t;
+
+/* FeedForward::from_source with Weights::Random (mlp.rs:18-37, mod.rs:38-45,
+ * 80-95): `{path}.gate`, `{path}.up`, `{path}.down`, each a xavier weight from
+ * path_seed(seed, key) and a zero bias, cast to `dtype`. */
+int nomas_ffn_from_random(const char *path, int64_t dim, int64_t hidden, int dtype,
+                          uint64_t seed, int device, nomas_ffn_t **out);
+
+/* FeedForward::from_source with Weights::Loaded over load_dit's cast
+ * (mlp.rs:18-37, weights.rs:105-145): reads `{path}.{gate,up,down}.{weight,bias}`
+ * from the safetensors files; missing keys are NOMAS_ERR_WEIGHT_KEY with the
+ * reference's message. */
+int nomas_ffn_from_safetensors(const char *const *files, int64_t n_files, const char *path,
+                               int64_t dim, int64_t hidden, int dtype, int device,
+                               nomas_ffn_t **out);
+
+/* Lin::load of materialised tensors (mod.rs:69-77): host arrays in the model
+ * dtype, reference layout gate/up (H, D) + (H), down (D, H) + (D); biases may
+ * be null (zero). */
+int nomas_ffn_from_host(int64_t dim, int64_t hidden, int dtype, int device, const void *gate_w,
+                        const void *gate_b, const void *up_w, const void *up_b,
+                        const void *down_w, const void *down_b, nomas_ffn_t **out);
+
+/* FeedForward::forward (mlp.rs:39-48) on device rows (x, y: rows x D, 16-byte
+ * aligned) on `stream`, and on host rows (copied in and out). */
+int nomas_ffn_forward(nomas_ffn_t *h, const void *x, void *y, int64_t rows, void *stream);
+int nomas_ffn_forward_host(nomas_ffn_t *h, const void *x, void *y, int64_t rows);
+
+/* FeedForward::n_params (mlp.rs:50-58). */
+int64_t nomas_ffn_n_params(const nomas_ffn_t *h);
+
+/* No counterpart: per-stage timing ([0, tile table, K-blocked copy of x,
+ * gemm_gate_up, gemm_down, 0]) and the GEMM path, as for the MoE handle. */
+int nomas_ffn_set_profiling(nomas_ffn_t *h, int enable);
+int nomas_ffn_stage_times(nomas_ffn_t *h, float *ms6);
+int nomas_ffn_uses_mfma(const nomas_ffn_t *h);
+
+void nomas_ffn_destroy(nomas_ffn_t *h);
+
 /* Message of the last failure on this thread ("" if none). */
 const char *nomas_moe_last_error(void);
 

@@ -13,7 +13,7 @@
  *   nomas-core/src/modules/mod.rs:47-55     Weights::path_seed (FNV-1a)
  *   nomas-core/src/modules/mod.rs:122-142   Lin::fwd  (x @ W^T + b, rows folded)
  *   nomas-core/src/modules/moe.rs:65-109    MoeLayer::forward
- *   nomas-core/src/modules/mlp.rs:42-46     FeedForward::SwiGlu
+ *   nomas-core/src/modules/mlp.rs:39-48     FeedForward::SwiGlu (orc_ffn_f64, and each expert)
  *
  * Two evaluation modes:
  *   - sparse f64  (orc_forward_sparse_f64): routing from f64 logits, only the
@@ -262,6 +262,24 @@ static void swiglu_row_f64(int64_t D, int64_t H, const float *x, const float *wg
                 s += a[h] * (double)dr[h];
         }
         y[d] = s;
+    }
+}
+
+/* FeedForward::SwiGlu::forward (mlp.rs:39-48) on the listed rows (NULL:
+ * 0..nrows-1), f64: the dense FFN of the blocks without MoE. */
+void orc_ffn_f64(int64_t D, int64_t H, const float *x, const float *wg, const float *bg,
+                 const float *wu, const float *bu, const float *wd, const float *bd,
+                 const int64_t *rows, int64_t nrows, double *out)
+{
+#pragma omp parallel
+    {
+        double *a = (double *)malloc(sizeof(double) * (size_t)H);
+#pragma omp for schedule(dynamic, 1)
+        for (int64_t r = 0; r < nrows; ++r) {
+            int64_t t = rows ? rows[r] : r;
+            swiglu_row_f64(D, H, x + t * D, wg, bg, wu, bu, wd, bd, a, out + r * D);
+        }
+        free(a);
     }
 }
 

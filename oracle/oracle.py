@@ -55,6 +55,8 @@ def lib():
     L.orc_forward_sparse_f64.argtypes = (
         [C.c_int64] * 4 + [C.c_void_p] * 8 + [C.c_double] + [C.c_void_p] * 6
         + [C.c_void_p, C.c_int64, _f64p, C.c_void_p, C.c_void_p, C.c_void_p])
+    L.orc_ffn_f64.restype = None
+    L.orc_ffn_f64.argtypes = [C.c_int64] * 2 + [C.c_void_p] * 7 + [C.c_void_p, C.c_int64, _f64p]
     L.orc_forward_dense_f32.restype = C.c_int
     L.orc_forward_dense_f32.argtypes = (
         [C.c_int64] * 5 + [C.c_void_p] * 8 + [C.c_double] + [C.c_void_p] * 6
@@ -163,6 +165,26 @@ def forward_sparse(x, p, k, rows=None, shared_dense=0.0, dense=None):
                                  float(shared_dense), *[_ptr(a) for a in dn],
                                  _ptr(rows_a), n, out, _ptr(idx), _ptr(w), _ptr(gap))
     return out, idx, w, gap
+
+
+def ffn(x, f, rows=None):
+    """f64 dense SwiGLU feed-forward (mlp.rs:39-48) of the given rows (all when None).
+
+    ``f`` holds f32 arrays in the reference layout: wg, wu (H,D), bg, bu (H,),
+    wd (D,H), bd (D,); missing biases are zero.  Returns out[n,D] f64.
+    """
+    x = _f32(x)
+    T, D = x.shape
+    H = f["wg"].shape[0]
+    arrs = [_f32(f.get(n)) for n in ("wg", "bg", "wu", "bu", "wd", "bd")]
+    if rows is None:
+        rows_a, n = None, T
+    else:
+        rows_a = np.ascontiguousarray(rows, dtype=np.int64)
+        n = rows_a.size
+    out = np.empty((n, D), np.float64)
+    lib().orc_ffn_f64(D, H, _ptr(x), *[_ptr(a) for a in arrs], _ptr(rows_a), n, out)
+    return out
 
 
 def forward_dense_f32(x, p, k, shared_dense=0.0, dense=None, return_weights=False):

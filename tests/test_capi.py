@@ -161,3 +161,77 @@ def test_dtype_helpers_round_to_nearest_even():
                                   torch.from_numpy(x).to(torch.bfloat16).float().numpy())
     hf = nm.to_model_dtype(x, "f16")
     np.testing.assert_array_equal(nm.widen(hf, "f16"), x.astype(np.float16).astype(np.float32))
+
+
+# ---- dense feed-forward (mlp.rs:9-59) ---------------------------------------
+
+@pytest.mark.parametrize("dim,hidden,dtype,msg", [
+    (60, 128, 0, "multiple of 8"), (64, 0, 1, "hidden"), (64, 128, 9, "dtype")])
+def test_ffn_create_rejects_invalid_shape_before_touching_the_gpu(dim, hidden, dtype, msg):
+    h = C.c_void_p()
+    rc = _lib.lib().nomas_ffn_from_random(b"blocks.0.mlp", dim, hidden, dtype, 1, 0, C.byref(h))
+    assert rc == 1, _lib.last_error()
+    assert msg in _lib.last_error()
+    assert not h.value
+
+
+def test_ffn_null_arguments_are_rejected():
+    L = _lib.lib()
+    h = C.c_void_p()
+    assert L.nomas_ffn_from_random(None, 64, 128, 0, 1, 0, C.byref(h)) == 2
+    assert L.nomas_ffn_from_host(64, 128, 0, 0, *([None] * 6), C.byref(h)) == 2
+    assert L.nomas_ffn_forward(None, None, None, 4, None) == 2
+    assert L.nomas_ffn_forward_host(None, None, None, 4) == 2
+    assert L.nomas_ffn_n_params(None) == -1
+    assert L.nomas_ffn_uses_mfma(None) == 0
+    L.nomas_ffn_destroy(None)  # no-op
+
+
+def _ffn_checkpoint(path, D, H, drop=(), reshape=None):
+    rng = np.random.default_rng(1)
+    t = {}
+    for lin, (o, i) in (("gate", (H, D)), ("up", (H, D)), ("down", (D, H))):
+        t[f"blocks.0.mlp.{lin}.weight"] = rng.standard_normal((o, i)).astype(np.float32)
+        t[f"blocks.0.mlp.{lin}.bias"] = rng.standard_normal(o).astype(np.float32)
+    for k in drop:
+        del t[k]
+    if reshape:
+        t[reshape] = t[reshape].reshape(-1)
+    save_file(t, path)
+    return t
+
+
+def _load_ffn(files, D=16, H=8, dtype=0):
+    arr = (C.c_char_p * len(files))(*[f.encode() for f in files])
+    h = C.c_void_p()
+    rc = _lib.lib().nomas_ffn_from_safetensors(arr, len(files), b"blocks.0.mlp", D, H, dtype, 0,
+                                               C.byref(h))
+    return rc, _lib.last_error()
+
+
+def test_ffn_checkpoint_missing_keys(tmp_path):
+    # FeedForward::from_source reads {path}.gate/up/down (mlp.rs:30-34)
+    f = str(tmp_path / "ffn.safetensors")
+    _ffn_checkpoint(f, 16, 8, drop=("blocks.0.mlp.up.bias", "blocks.0.mlp.down.weight"))
+    rc, msg = _load_ffn([f])
+    assert rc == 3
+    assert "missing 2 model keys" in msg
+    assert msg.index("blocks.0.mlp.down.weight") < msg.index("blocks.0.mlp.up.bias")  # sorted
+
+
+def test_ffn_checkpoint_misshaped_tensor(tmp_path):
+    f = str(tmp_path / "ffn.safetensors")
+    _ffn_checkpoint(f, 16, 8, reshape="blocks.0.mlp.gate.weight")
+    rc, msg = _load_ffn([f])
+    assert rc == 3 and "gate.weight" in msg
+
+
+def test_ffn_complete_checkpoint_parses_then_needs_a_device(tmp_path):
+    f = str(tmp_path / "ffn.safetensors")
+    _ffn_checkpoint(f, 16, 8)
+    rc, msg = _load_ffn([f])
+    import torch
+    if torch.cuda.is_available():
+        assert rc == 0, msg
+    else:
+        assert rc == 5 and "HIP device" in msg

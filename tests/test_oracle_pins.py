@@ -274,12 +274,35 @@ def pin_shared_dense_branch():
     np.testing.assert_allclose(got, want, rtol=1e-10, atol=1e-12)
 
 
+def pin_ffn_bruteforce():
+    # FeedForward::SwiGlu (mlp.rs:39-48) against an independent torch f64 evaluation
+    D, H = 20, 28
+    f = {k: v[0] for k, v in _params(31, 1, D, H).items() if k != "wr"}
+    x = np.random.default_rng(32).standard_normal((9, D)).astype(np.float32)
+    want = _torch_ffn(x, f["wg"], f["bg"], f["wu"], f["bu"], f["wd"], f["bd"])
+    np.testing.assert_allclose(O.ffn(x, f), want, rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(O.ffn(x, f, rows=[7, 2]), want[[7, 2]], rtol=1e-10, atol=1e-12)
+
+
+def pin_ffn_equals_single_expert():
+    # one expert, top-1: every row routed with gate p / (p + 1e-9), p = 1
+    D, H = 12, 16
+    p = _params(33, 1, D, H)
+    f = {k: v[0] for k, v in p.items() if k != "wr"}
+    x = np.random.default_rng(34).standard_normal((5, D)).astype(np.float32)
+    moe, idx, w, _ = O.forward_sparse(x, p, 1)
+    assert (idx == 0).all()
+    np.testing.assert_allclose(w, 1.0 / (1.0 + 1e-9), rtol=0, atol=1e-15)
+    np.testing.assert_allclose(O.ffn(x, f), moe * (1.0 + 1e-9), rtol=1e-12, atol=1e-14)
+
+
 PINS = [pin_splitmix64, pin_fnv1a, pin_box_muller, pin_affine_and_moments, pin_uniform,
         pin_xavier_std,
         pin_bf16_rounding, pin_route_bruteforce, pin_route_ties_lowest_index,
         pin_route_one_hot_rows, pin_route_weights_sum_to_one, pin_forward_bruteforce,
         pin_dense_equals_sparse, pin_k_equals_experts, pin_single_dominant_expert,
-        pin_zero_input_zero_output, pin_row_permutation, pin_shared_dense_branch]
+        pin_zero_input_zero_output, pin_row_permutation, pin_shared_dense_branch,
+        pin_ffn_bruteforce, pin_ffn_equals_single_expert]
 
 
 @pytest.mark.parametrize("pin", PINS, ids=[p.__name__ for p in PINS])
