@@ -94,6 +94,47 @@ def cpu_baseline(w, params, x, target_s=12.0):
     }
 
 
+def bench_ffn(args, w) -> int:
+    """The dense SwiGLU feed-forward (FeedForward::SwiGlu) at the workload's shape."""
+    import numpy as np
+    import torch
+    import nomas_moe as nm
+
+    dt = nm.DataType.of(w.dtype)
+    ffn = nm.FeedForward.from_source(nm.Weights.random(0x5EED0000, dt), "blocks.0.mlp", w.dim,
+                                     w.hidden)
+    raw = nm.to_model_dtype(nm.randn_affine(0x5EED0001, w.rows * w.dim).reshape(w.rows, w.dim), dt)
+    xd = torch.from_numpy(raw.view(np.int16) if raw.dtype == np.uint16 else raw)
+    xd = xd.view(dt.torch).cuda()
+    y = torch.empty_like(xd)
+    for _ in range(args.warmup):
+        ffn.forward(xd, out=y)
+    torch.cuda.synchronize()
+    ffn.set_profiling(True)
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+        ffn.forward(xd, out=y)
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    st = ffn.stage_times()
+    flops = 6.0 * w.rows * w.dim * w.hidden
+    gemm_ms = st["gemm_gate_up"] + st["gemm_down"]
+    print(json.dumps({
+        "metric": f"dense SwiGLU FFN tokens/s at dim{w.dim} hidden{w.hidden} {w.dtype}",
+        "value": w.rows / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "dtype": w.dtype,
+        "data": "synthetic (seeded N(0,1) rows, random-init weights)",
+        "config": {"workload": f"dense FFN, {w.rows} rows", "rows": w.rows, "dim": w.dim,
+                   "hidden": w.hidden},
+        "stages_ms": st, "gemm_tflops": flops / (gemm_ms * 1e-3) / 1e12,
+        "gemm_frac": flops / (gemm_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+        "uses_mfma": ffn.uses_mfma}))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -101,6 +142,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="cfg8b")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--ffn", action="store_true",
+                    help="time the dense SwiGLU feed-forward (one expert, no routing) at the "
+                         "workload's dim, hidden and rows instead of the MoE block")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only run a plain copy of this many MB (counter calibration) and exit")
     args = ap.parse_args()
@@ -117,6 +161,8 @@ def main() -> int:
     from nomas_moe import workloads as wl
 
     w = wl.WORKLOADS[args.workload]
+    if args.ffn:
+        return bench_ffn(args, w)
     dt = nm.DataType.of(w.dtype)
     print(f"[bench] workload {w.name}: rows={w.rows} D={w.dim} E={w.experts} k={w.top_k} "
           f"H={w.hidden} {w.dtype}", file=sys.stderr, flush=True)
