@@ -9,6 +9,7 @@ scan, dispatch, gate/up GEMM, down GEMM, combine) with x already resident in
 HBM.  Prints one JSON line.
 
   python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
+                  [--ffn | --block]
 """
 from __future__ import annotations
 
@@ -135,6 +136,64 @@ def bench_ffn(args, w) -> int:
     return 0
 
 
+def bench_block(args, w) -> int:
+    """The FFN half of the DiT block around the MoE (block.rs:96-101) --
+    norm2 + modulate, the MoE, the gated residual -- against the plain MoE
+    forward on the same rows."""
+    import numpy as np
+    import torch
+    import nomas_moe as nm
+    from nomas_moe import workloads as wl
+
+    dt = nm.DataType.of(w.dtype)
+    B, S, D = w.sequences, w.rows // w.sequences, w.dim
+    params = wl.make_params(w)
+    cfg = nm.MoeConfig(w.experts, w.top_k, 0.0, 0)
+    layer = nm.MoeLayer.from_source(nm.Weights.from_tensors(params, dt), wl.moe_path(), D,
+                                    w.hidden, cfg)
+    raw = nm.to_model_dtype(wl.make_x(w), dt)
+    xd = torch.from_numpy(raw.view(np.int16) if raw.dtype == np.uint16 else raw)
+    xd = xd.view(dt.torch).cuda().reshape(B, S, D)
+    rnd = lambda seed, n, std: torch.from_numpy(nm.randn_affine(seed, n, 0.0, std)).cuda()
+    shift, scale, gate = (rnd(w.base_seed + i, B * D, 0.5).reshape(B, D) for i in (1, 2, 3))
+    norm_w = rnd(w.base_seed + 4, D, 1.0)
+    out = torch.empty_like(xd)
+    stream = torch.cuda.current_stream()
+
+    def timed(fn):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(args.steps):
+            fn()
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / args.steps
+
+    ms_block = timed(lambda: layer.forward_block(xd, shift, scale, gate, norm_w, out=out))
+    ms_plain = timed(lambda: layer.forward(xd, out=out))
+    ms_seam = timed(lambda: nm.norm_modulate(xd, shift, scale, norm_w, out=out))
+    b = 2 if w.dtype != "f32" else 4
+    print(json.dumps({
+        "metric": f"DiT block FFN half (norm2 + modulate, MoE, gated residual) tokens/s at "
+                  f"dim{D} E{w.experts} top{w.top_k} {w.dtype}",
+        "value": w.rows / (ms_block * 1e-3), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_block,
+        "higher_is_better": True, "dtype": w.dtype,
+        "data": "synthetic (seeded N(0,1) rows, random-init weights, N(0,0.25) AdaLN parameters)",
+        "config": {"workload": f"{w.name}: {w.note}", "sequences": B, "seq_len": S, "dim": D,
+                   "experts": w.experts, "top_k": w.top_k, "hidden": w.hidden},
+        "plain_moe_ms": ms_plain, "seam_overhead_ms": ms_block - ms_plain,
+        "norm_modulate_ms": ms_seam,
+        # norm_modulate alone: reads x twice (once through the sum of squares,
+        # once for h) and writes h
+        "norm_modulate_hbm_gbps": 3.0 * w.rows * D * b / (ms_seam * 1e-3) / 1e9,
+    }))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -145,6 +204,9 @@ def main() -> int:
     ap.add_argument("--ffn", action="store_true",
                     help="time the dense SwiGLU feed-forward (one expert, no routing) at the "
                          "workload's dim, hidden and rows instead of the MoE block")
+    ap.add_argument("--block", action="store_true",
+                    help="time the FFN half of the DiT block (norm2 + modulate, MoE, gated "
+                         "residual) against the plain MoE forward")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only run a plain copy of this many MB (counter calibration) and exit")
     args = ap.parse_args()
@@ -163,6 +225,8 @@ def main() -> int:
     w = wl.WORKLOADS[args.workload]
     if args.ffn:
         return bench_ffn(args, w)
+    if args.block:
+        return bench_block(args, w)
     dt = nm.DataType.of(w.dtype)
     print(f"[bench] workload {w.name}: rows={w.rows} D={w.dim} E={w.experts} k={w.top_k} "
           f"H={w.hidden} {w.dtype}", file=sys.stderr, flush=True)

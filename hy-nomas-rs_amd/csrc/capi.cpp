@@ -266,6 +266,21 @@ int nomas_moe_forward(nomas_moe_t* h, const void* x, void* y, int64_t rows, void
     return h->layer->forward(x, y, rows, static_cast<hipStream_t>(stream));
 }
 
+int nomas_moe_forward_block(nomas_moe_t* h, const void* x, void* out, int64_t rows, int64_t seq,
+                            const float* norm_w, double eps, const float* shift,
+                            const float* scale, const float* gate, void* stream) {
+    nomas::clear_error();
+    if (!h) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "null handle");
+    MoeLayer::BlockArgs b;
+    b.seq = seq;
+    b.norm_w = norm_w;
+    b.eps = eps;
+    b.shift = shift;
+    b.scale = scale;
+    b.gate = gate;
+    return h->layer->forward_block(x, out, rows, b, static_cast<hipStream_t>(stream));
+}
+
 int nomas_moe_forward_host(nomas_moe_t* h, const void* x, void* y, int64_t rows) {
     nomas::clear_error();
     if (!h) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "null handle");
@@ -422,6 +437,70 @@ int nomas_ffn_stage_times(nomas_ffn_t* h, float* ms6) {
 int nomas_ffn_uses_mfma(const nomas_ffn_t* h) { return h && h->layer->uses_mfma() ? 1 : 0; }
 
 void nomas_ffn_destroy(nomas_ffn_t* h) { delete h; }
+
+namespace {
+
+int check_seam_args(int dtype, const void* a, const void* b, const void* c, int64_t rows,
+                    int64_t dim, int64_t seq) {
+    if (dtype < 0 || dtype > 2) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
+    if (rows < 0) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "rows must be >= 0");
+    if (dim <= 0 || dim % 8 != 0 || dim > (1 << 24))
+        return set_error(NOMAS_ERR_INVALID_ARGUMENT, "dim must be a positive multiple of 8 (got %lld)",
+                         (long long)dim);
+    if (seq < 1 || rows % seq != 0)
+        return set_error(NOMAS_ERR_INVALID_ARGUMENT,
+                         "rows=%lld must be a whole number of sequences of seq=%lld",
+                         (long long)rows, (long long)seq);
+    if (rows == 0) return NOMAS_OK;
+    if (!a || !b || !c) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "null tensor pointer");
+    if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+         reinterpret_cast<uintptr_t>(c)) & 15)
+        return set_error(NOMAS_ERR_INVALID_ARGUMENT, "tensors must be 16-byte aligned");
+    return NOMAS_OK;
+}
+
+}  // namespace
+
+int nomas_norm_modulate(int dtype, const void* x, void* h, int64_t rows, int64_t dim, int64_t seq,
+                        const float* norm_w, double eps, const float* shift, const float* scale,
+                        void* stream) {
+    nomas::clear_error();
+    int rc = check_seam_args(dtype, x, h, shift, rows, dim, seq);
+    if (rc != NOMAS_OK || rows == 0) return rc;
+    if (!scale) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "scale must be non-null");
+    if ((reinterpret_cast<uintptr_t>(scale) | reinterpret_cast<uintptr_t>(norm_w)) & 15)
+        return set_error(NOMAS_ERR_INVALID_ARGUMENT, "scale and norm_w must be 16-byte aligned");
+    if (!(eps >= 0.0)) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "eps must be >= 0");
+    nomas::SeamArgs a;
+    a.x = x;
+    a.h = h;
+    a.rows = rows;
+    a.D = (int)dim;
+    a.seq = seq;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.shift = shift;
+    a.scale = scale;
+    hipError_t e = nomas::launch_seam_h(static_cast<DType>(dtype), a, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess)
+        return set_error(NOMAS_ERR_HIP, "norm/modulate launch failed: %s", hipGetErrorString(e));
+    return NOMAS_OK;
+}
+
+int nomas_gated_residual(int dtype, const void* x, const void* y, const float* gate, void* out,
+                         int64_t rows, int64_t dim, int64_t seq, void* stream) {
+    nomas::clear_error();
+    int rc = check_seam_args(dtype, x, y, out, rows, dim, seq);
+    if (rc != NOMAS_OK || rows == 0) return rc;
+    if (!gate) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "gate must be non-null");
+    if (reinterpret_cast<uintptr_t>(gate) & 15)
+        return set_error(NOMAS_ERR_INVALID_ARGUMENT, "gate must be 16-byte aligned");
+    hipError_t e = nomas::launch_gated_residual(static_cast<DType>(dtype), x, y, gate, out, rows,
+                                                (int)dim, seq, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess)
+        return set_error(NOMAS_ERR_HIP, "gated residual launch failed: %s", hipGetErrorString(e));
+    return NOMAS_OK;
+}
 
 const char* nomas_moe_last_error(void) { return nomas::last_error(); }
 

@@ -10,6 +10,7 @@
 #include <algorithm>
 
 #include "kernels.hpp"
+#include "seam.hpp"
 
 namespace nomas {
 
@@ -195,8 +196,12 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     const int k = a.k_slots;
     const T* y = static_cast<const T*>(a.y_perm);
     T* out = static_cast<T*>(a.out);
+    // gated residual: the row's gate and input (block.rs:101)
+    const float* grow = a.gate ? a.gate + row / a.seq * a.D : nullptr;
+    const T* xrow = a.gate ? static_cast<const T*>(a.resid_x) + row * a.D : nullptr;
     for (int c = lane; c < nchunk; c += kWave) {
-        float acc[EPC];
+        float acc[EPC], xv[EPC];
+        if (grow) load16(xrow + (int64_t)c * EPC, xv);  // in flight with the y loads
 #pragma unroll
         for (int i = 0; i < EPC; ++i) acc[i] = 0.0f;
         for (int j = 0; j < k; ++j) {
@@ -207,6 +212,13 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
             load16(y + (int64_t)p * a.D + (int64_t)c * EPC, v);
 #pragma unroll
             for (int i = 0; i < EPC; ++i) acc[i] = acc[i] + v[i] * w;
+        }
+        if (grow) {  // out = x + y * gate, y and each step rounded to the model dtype
+            float g[EPC];
+            load_f32s<EPC>(grow + (int64_t)c * EPC, g);
+#pragma unroll
+            for (int i = 0; i < EPC; ++i)
+                acc[i] = seam_residual<T>(xv[i], Elt<T>::to_f32(Elt<T>::from_f32(acc[i])), g[i]);
         }
         store16(out + row * a.D + (int64_t)c * EPC, acc);
     }

@@ -83,6 +83,19 @@ public:
     int upload_f32(const MoeParamsF32& p);
 
     int forward(const void* x, void* y, int64_t rows, hipStream_t s);
+    // The FFN half of a DiT block around the MoE (block.rs:96-101):
+    // out = x + moe(modulate(norm2(x), shift, scale)) * gate, with (rows / seq,
+    // D) f32 shift / scale / gate and an optional f32 norm gain, all device
+    // pointers.  out may alias x.
+    struct BlockArgs {
+        int64_t seq;
+        const float* norm_w;
+        double eps;
+        const float* shift;
+        const float* scale;
+        const float* gate;
+    };
+    int forward_block(const void* x, void* out, int64_t rows, const BlockArgs& b, hipStream_t s);
     int forward_host(const void* x, void* y, int64_t rows);
     int routing(int32_t* idx, float* w, int32_t* counts, float* gap);
     int set_profiling(bool on);
@@ -111,6 +124,8 @@ private:
     int BM_;
     bool dense_only_ = false;
     int forward_dense(const void* x, void* y, int64_t rows, hipStream_t s);
+    int forward_impl(const void* x, void* y, int64_t rows, hipStream_t s, const BlockArgs* blk);
+    bool want_block_ = false;  // the workspace holds h for forward_block
 
     // device weights
     void* d_wr_ = nullptr;
@@ -135,6 +150,7 @@ private:
     void* d_xperm_ = nullptr;
     void* d_h_ = nullptr;
     void* d_yperm_ = nullptr;
+    void* d_block_h_ = nullptr;       // forward_block: h = modulate(norm2(x)), rows x D
     float* d_split_ws_ = nullptr;     // MFMA path: partial tiles of K-split GEMM tails
     int32_t* d_split_cnt_ = nullptr;  // their arrival counters
 

@@ -20,6 +20,25 @@ constexpr int kMfmaBM = 256;
 constexpr int kMfmaBN = 256;
 constexpr int kSimtBM = 64;
 
+// The FFN half of a DiT block around the MoE (block.rs:96-101):
+//   h   = modulate(norm2(x), shift, scale)   (norm.rs:55-65, modulate.rs:69-79)
+//   out = x + moe(h) * gate
+// Row r belongs to sequence r / seq; shift, scale, gate are (sequences, D) f32.
+// seam_h_kernel writes h (read by the router and the dispatch as their x);
+// the combine applies the gated residual in its epilogue.
+struct SeamArgs {
+    const void* x;        // rows x D, model dtype
+    void* h;              // rows x D, model dtype
+    int64_t rows;
+    int D;
+    int64_t seq;          // rows per sequence
+    const float* norm_w;  // D (null: no affine gain)
+    double eps;
+    const float* shift;   // sequences x D
+    const float* scale;
+    int factor_lds;       // set by the launcher: LDS bytes for the factors
+};
+
 struct RouterArgs {
     const void* x;
     const void* wr;
@@ -95,10 +114,17 @@ struct CombineArgs {
     int D, k_slots;
     void* out;
     int64_t a_cap;  // rows of y_perm
+    // gated residual (gate non-null): out = x + out_moe * gate[row / seq]
+    const void* resid_x;  // rows x D, model dtype
+    const float* gate;    // sequences x D
+    int64_t seq;
 };
 
 size_t router_lds_bytes(int E);
 
+hipError_t launch_seam_h(DType dt, const SeamArgs& a, hipStream_t s);
+hipError_t launch_gated_residual(DType dt, const void* x, const void* y, const float* gate,
+                                 void* out, int64_t rows, int D, int64_t seq, hipStream_t s);
 hipError_t launch_router(DType dt, const RouterArgs& a, hipStream_t s);
 hipError_t launch_scan(const ScanArgs& a, hipStream_t s);
 hipError_t launch_dispatch(DType dt, const DispatchArgs& a, hipStream_t s);

@@ -270,11 +270,13 @@ int MoeLayer::max_tiles(int64_t rows) const {
 void MoeLayer::free_workspace() {
     if (d_ws_) (void)hipFree(d_ws_);
     d_ws_ = nullptr;
+    d_block_h_ = nullptr;
     cap_rows_ = 0;
+    last_rows_ = -1;  // the last forward's routing went with the buffers
 }
 
 int MoeLayer::ensure_workspace(int64_t rows) {
-    if (rows <= cap_rows_) return NOMAS_OK;
+    if (rows <= cap_rows_ && (!want_block_ || d_block_h_)) return NOMAS_OK;
     int64_t cap = std::max<int64_t>(rows, cap_rows_ + cap_rows_ / 2);
     cap = (cap + kRouterRows - 1) / kRouterRows * kRouterRows;
     const int64_t A = cap * kslots_;
@@ -296,6 +298,7 @@ int MoeLayer::ensure_workspace(int64_t rows) {
     const size_t o_xp = take(es * A * D_);
     const size_t o_h = take(es * A * H_);
     const size_t o_yp = dense_only_ ? 0 : take(es * A * D_);  // dense: the down GEMM writes y
+    const size_t o_bh = want_block_ ? take(es * cap * D_) : 0;
     const size_t o_sw = mfma_ ? take(sizeof(float) * kSplitUnitFloats * kSplitUnits) : 0;
     const size_t o_sc = mfma_ ? take(sizeof(int32_t) * kSplitUnits) : 0;
     free_workspace();
@@ -322,6 +325,7 @@ int MoeLayer::ensure_workspace(int64_t rows) {
     d_xperm_ = b + o_xp;
     d_h_ = b + o_h;
     d_yperm_ = dense_only_ ? nullptr : b + o_yp;
+    d_block_h_ = want_block_ ? b + o_bh : nullptr;
     d_split_ws_ = mfma_ ? reinterpret_cast<float*>(b + o_sw) : nullptr;
     d_split_cnt_ = mfma_ ? reinterpret_cast<int32_t*>(b + o_sc) : nullptr;
     cap_rows_ = cap;
@@ -331,6 +335,28 @@ int MoeLayer::ensure_workspace(int64_t rows) {
 // ---- forward ------------------------------------------------------------------
 
 int MoeLayer::forward(const void* x, void* y, int64_t rows, hipStream_t s) {
+    return forward_impl(x, y, rows, s, nullptr);
+}
+
+int MoeLayer::forward_block(const void* x, void* out, int64_t rows, const BlockArgs& b,
+                            hipStream_t s) {
+    if (!b.shift || !b.scale || !b.gate)
+        return set_error(NOMAS_ERR_INVALID_ARGUMENT, "shift, scale and gate must be non-null");
+    if (b.seq < 1 || rows % b.seq != 0)
+        return set_error(NOMAS_ERR_INVALID_ARGUMENT,
+                         "rows=%lld must be a whole number of sequences of seq=%lld",
+                         (long long)rows, (long long)b.seq);
+    if (!(b.eps >= 0.0)) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "eps must be >= 0");
+    if ((reinterpret_cast<uintptr_t>(b.shift) | reinterpret_cast<uintptr_t>(b.scale) |
+         reinterpret_cast<uintptr_t>(b.gate) | reinterpret_cast<uintptr_t>(b.norm_w)) & 15)
+        return set_error(NOMAS_ERR_INVALID_ARGUMENT,
+                         "shift, scale, gate and norm_w must be 16-byte aligned");
+    want_block_ = true;  // the next workspace layout holds h
+    return forward_impl(x, out, rows, s, &b);
+}
+
+int MoeLayer::forward_impl(const void* x, void* y, int64_t rows, hipStream_t s,
+                           const BlockArgs* blk) {
     if (rows < 0) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "rows must be >= 0 (got %lld)", (long long)rows);
     if (rows == 0) { last_rows_ = 0; return NOMAS_OK; }
     if (!x || !y) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "x and y must be non-null");
@@ -344,7 +370,10 @@ int MoeLayer::forward(const void* x, void* y, int64_t rows, hipStream_t s) {
     int rc = ensure_workspace(rows);
     if (rc != NOMAS_OK) return rc;
     if (done_recorded_ && s != last_stream_) HIP_TRY(hipStreamWaitEvent(s, done_, 0));
-    if (dense_only_) return forward_dense(x, y, rows, s);
+    if (dense_only_) {
+        if (blk) return set_error(NOMAS_ERR_STATE, "the fused block is implemented for the MoE layer");
+        return forward_dense(x, y, rows, s);
+    }
 
     const int nch = (int)((rows + kRouterRows - 1) / kRouterRows);
     const int mt = max_tiles(rows);
@@ -365,8 +394,23 @@ int MoeLayer::forward(const void* x, void* y, int64_t rows, hipStream_t s) {
     } while (0)
 
     if ((rc = mark(0))) return rc;
+    const void* xr = x;  // what the router and the dispatch read: x, or h in a block
+    if (blk) {
+        SeamArgs sm;
+        sm.x = x;
+        sm.h = d_block_h_;
+        sm.rows = rows;
+        sm.D = (int)D_;
+        sm.seq = blk->seq;
+        sm.norm_w = blk->norm_w;
+        sm.eps = blk->eps;
+        sm.shift = blk->shift;
+        sm.scale = blk->scale;
+        STAGE(launch_seam_h(dt_, sm, s), "norm/modulate");
+        xr = d_block_h_;
+    }
     RouterArgs ra;
-    ra.x = x;
+    ra.x = xr;
     ra.wr = d_wr_;
     ra.rows = rows;
     ra.D = (int)D_;
@@ -396,7 +440,7 @@ int MoeLayer::forward(const void* x, void* y, int64_t rows, hipStream_t s) {
     if ((rc = mark(2))) return rc;
 
     DispatchArgs da;
-    da.x = x;
+    da.x = xr;
     da.rows = rows;
     da.D = (int)D_;
     da.E_cols = (int)Ecols_;
@@ -448,6 +492,9 @@ int MoeLayer::forward(const void* x, void* y, int64_t rows, hipStream_t s) {
     ca.k_slots = (int)kslots_;
     ca.out = y;
     ca.a_cap = cap_rows_ * kslots_;
+    ca.resid_x = blk ? x : nullptr;
+    ca.gate = blk ? blk->gate : nullptr;
+    ca.seq = blk ? blk->seq : 1;
     STAGE(launch_combine(dt_, ca, s), "combine");
     if ((rc = mark(6))) return rc;
 #undef STAGE

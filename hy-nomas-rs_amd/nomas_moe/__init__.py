@@ -27,7 +27,8 @@ from ._lib import nomas_moe_config
 
 __all__ = [
     "DataType", "MoeConfig", "Weights", "MoeLayer", "FeedForward", "NomasError", "InvalidConfig",
-    "WeightKey", "IoError", "path_seed", "randn_affine", "to_model_dtype",
+    "WeightKey", "IoError", "path_seed", "randn_affine", "to_model_dtype", "norm_modulate",
+    "gated_residual",
 ]
 
 
@@ -130,6 +131,72 @@ def widen(a: np.ndarray, dtype) -> np.ndarray:
     if dt == DataType.Bf16:
         return (np.asarray(a, np.uint16).astype(np.uint32) << 16).view(np.float32)
     return np.asarray(a, np.uint16).view(np.float16).astype(np.float32)
+
+
+def _seam_params(x: torch.Tensor, named) -> list:
+    """(B, D) AdaLN parameters (and an optional (D,) gain) as contiguous f32 on x's device."""
+    B, _, D = x.shape
+    out = []
+    for name, t, shape in named:
+        if t is None:
+            out.append(None)
+            continue
+        if tuple(t.shape) != shape(B, D):
+            raise NomasError(2, f"{name}: expected {shape(B, D)}, got {tuple(t.shape)}")
+        out.append(t.to(device=x.device, dtype=torch.float32).contiguous())
+    return out
+
+
+def _seam_input(x: torch.Tensor) -> torch.Tensor:
+    if x.dim() != 3:
+        raise NomasError(2, f"expected (B, L, D) activations, got shape {tuple(x.shape)}")
+    if not x.is_cuda:
+        raise NomasError(2, "the block seams take device tensors")
+    DataType.of(x.dtype)
+    return x.contiguous()
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def norm_modulate(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor,
+                  norm_w: torch.Tensor | None = None, eps: float = 1e-6,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """h = modulate(norm2(x), shift, scale) (block.rs:96; norm.rs:55-65,
+    modulate.rs:69-79).  x: (B, L, D) device tensor in f32 / bf16 / f16;
+    shift / scale: (B, D); norm_w: (D,) or None (RmsNorm::no_affine)."""
+    xc = _seam_input(x)
+    B, S, D = xc.shape
+    sh, sc, nw = _seam_params(xc, (("shift", shift, lambda b, d: (b, d)),
+                                   ("scale", scale, lambda b, d: (b, d)),
+                                   ("norm_w", norm_w, lambda b, d: (d,))))
+    if out is None:
+        out = torch.empty_like(xc)
+    stream = torch.cuda.current_stream(xc.device).cuda_stream
+    _check(_lib.lib().nomas_norm_modulate(int(DataType.of(xc.dtype)), xc.data_ptr(),
+                                          out.data_ptr(), B * S, D, max(S, 1), _ptr(nw),
+                                          float(eps), sh.data_ptr(), sc.data_ptr(), stream))
+    return out
+
+
+def gated_residual(x: torch.Tensor, y: torch.Tensor, gate: torch.Tensor,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """out = x + y * gate (block.rs:101).  x, y: (B, L, D) device tensors of one
+    dtype; gate: (B, D)."""
+    xc = _seam_input(x)
+    if tuple(y.shape) != tuple(xc.shape) or y.dtype != xc.dtype:
+        raise NomasError(2, "y must match x in shape and dtype")
+    yc = y.contiguous()
+    B, S, D = xc.shape
+    (g,) = _seam_params(xc, (("gate", gate, lambda b, d: (b, d)),))
+    if out is None:
+        out = torch.empty_like(xc)
+    stream = torch.cuda.current_stream(xc.device).cuda_stream
+    _check(_lib.lib().nomas_gated_residual(int(DataType.of(xc.dtype)), xc.data_ptr(),
+                                           yc.data_ptr(), g.data_ptr(), out.data_ptr(), B * S, D,
+                                           max(S, 1), stream))
+    return out
 
 
 class Weights:
@@ -274,6 +341,31 @@ class MoeLayer:
         return out
 
     __call__ = forward
+
+    # -- the FFN half of DiTBlock::forward (block.rs:96-101) ------------------
+    def forward_block(self, x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor,
+                      gate: torch.Tensor, norm_w: torch.Tensor | None = None, eps: float = 1e-6,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+        """x + moe(modulate(norm2(x), shift, scale)) * gate: the FFN half of
+        DiTBlock::forward (block.rs:96-101) around this MoE.  x: (B, L, D) in
+        the model dtype on the layer's GPU; shift / scale / gate: (B, D);
+        norm_w: (D,) or None (no affine gain).  out may be x (in place)."""
+        xc = _seam_input(x)
+        if xc.shape[-1] != self.dim or xc.dtype != self.dtype.torch:
+            raise NomasError(2, f"expected (B, L, {self.dim}) {self.dtype.torch}, got "
+                                f"{tuple(x.shape)} {x.dtype}")
+        B, S, D = xc.shape
+        sh, sc, g, nw = _seam_params(xc, (("shift", shift, lambda b, d: (b, d)),
+                                          ("scale", scale, lambda b, d: (b, d)),
+                                          ("gate", gate, lambda b, d: (b, d)),
+                                          ("norm_w", norm_w, lambda b, d: (d,))))
+        if out is None:
+            out = torch.empty_like(xc)
+        stream = torch.cuda.current_stream(xc.device).cuda_stream
+        _check(_lib.lib().nomas_moe_forward_block(
+            self._h, xc.data_ptr(), out.data_ptr(), B * S, max(S, 1), _ptr(nw), float(eps),
+            sh.data_ptr(), sc.data_ptr(), g.data_ptr(), stream))
+        return out
 
     def n_params(self) -> int:
         """moe.rs:112-114."""

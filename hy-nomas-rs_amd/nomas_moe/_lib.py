@@ -51,6 +51,8 @@ def lib() -> C.CDLL:
     L.nomas_moe_from_host.restype = i32
     L.nomas_moe_forward.argtypes = [vp, vp, vp, i64, vp]
     L.nomas_moe_forward.restype = i32
+    L.nomas_moe_forward_block.argtypes = [vp, vp, vp, i64, i64, vp, C.c_double, vp, vp, vp, vp]
+    L.nomas_moe_forward_block.restype = i32
     L.nomas_moe_forward_host.argtypes = [vp, vp, vp, i64]
     L.nomas_moe_forward_host.restype = i32
     L.nomas_moe_n_params.argtypes = [vp]
@@ -86,6 +88,10 @@ def lib() -> C.CDLL:
     L.nomas_ffn_stage_times.restype = i32
     L.nomas_ffn_uses_mfma.argtypes = [vp]
     L.nomas_ffn_uses_mfma.restype = i32
+    L.nomas_norm_modulate.argtypes = [i32, vp, vp, i64, i64, i64, vp, C.c_double, vp, vp, vp]
+    L.nomas_norm_modulate.restype = i32
+    L.nomas_gated_residual.argtypes = [i32, vp, vp, vp, vp, i64, i64, i64, vp]
+    L.nomas_gated_residual.restype = i32
     L.nomas_ffn_destroy.argtypes = [vp]
     L.nomas_ffn_destroy.restype = None
     L.nomas_moe_last_error.argtypes = []

@@ -44,6 +44,7 @@ class Workload:
     dtype: str
     router: str = "normal"  # normal | fine64 | skewed16
     note: str = ""
+    sequences: int = 1  # the batch of the DiT block the rows come from (rows / seq)
 
     @property
     def base_seed(self) -> int:
@@ -65,7 +66,8 @@ WORKLOADS = {
         Workload("seg8b", 1, 4680, 3072, 8, 2, 8192, "bf16",
                  note="8B preset, one segment: 3 latent frames x 1560 rows"),
         Workload("cfg8b", 2, 14232, 3072, 8, 2, 8192, "bf16",
-                 note="8B preset, three guidance branches stacked: 3 x (4680 video + 64 text)"),
+                 note="8B preset, three guidance branches stacked: 3 x (4680 video + 64 text)",
+                 sequences=3),
         Workload("fine64", 3, 16384, 3072, 64, 8, 1536, "bf16", router="fine64",
                  note="fine-grained: 64 experts, top-8, per-expert logit bias N(0, 0.5)"),
         Workload("skewed16", 4, 32768, 3072, 16, 2, 4096, "bf16", router="skewed16",

@@ -96,6 +96,29 @@ int nomas_moe_from_host(const nomas_moe_config *cfg, int64_t dim, int64_t hidden
  * hipStream_t (NULL = default stream).  Asynchronous with respect to the host. */
 int nomas_moe_forward(nomas_moe_t *h, const void *x, void *y, int64_t rows, void *stream);
 
+/* The FFN half of DiTBlock::forward around the MoE (block.rs:96-101), fused
+ * into the MoE's own kernels:
+ *   h   = modulate(norm2(x), shift, scale)     (norm.rs:55-65, modulate.rs:69-79)
+ *   out = x + moe(h) * gate
+ * x and out are (rows, D) in the handle's dtype, device-resident, 16-byte
+ * aligned (out may alias x); row r belongs to sequence r / seq (rows must be a
+ * multiple of seq).  shift, scale and gate are (rows / seq, D) f32 on the
+ * device, 16-byte aligned: the AdaLN parameters of the batch (AdaSix::{shift,scale,gate}_mlp,
+ * modulate.rs:13-27).  norm_w is norm2's affine gain widened to f32 (D
+ * entries) or NULL for RmsNorm::no_affine; eps is norm2's (1e-6 in
+ * DiTBlock::from_source, block.rs:56-57).  Rounding to the model dtype happens
+ * where the reference's to_dtype casts do (after the norm, after modulate, on
+ * the MoE output, on y * gate and on the sum); the row's sum of squares is
+ * accumulated in f64.  For an F32 handle this is the reference's arithmetic;
+ * for BF16/F16 the reference's modulate (an F32 tensor times model-dtype
+ * parameters) does not type-check in candle, and this entry point defines the
+ * block with the f32 parameters above.  The router sees h, so routing()
+ * reports h's routing; with shared_dense > 0 the dense branch reads h too.
+ * Dense (nomas_ffn_t) handles have no fused block. */
+int nomas_moe_forward_block(nomas_moe_t *h, const void *x, void *out, int64_t rows, int64_t seq,
+                            const float *norm_w, double eps, const float *shift,
+                            const float *scale, const float *gate, void *stream);
+
 /* MoeLayer::forward on host tensors (the candle CPU-tensor case): copies x in,
  * runs the forward, copies y out and synchronises. */
 int nomas_moe_forward_host(nomas_moe_t *h, const void *x, void *y, int64_t rows);
@@ -171,6 +194,26 @@ int nomas_ffn_stage_times(nomas_ffn_t *h, float *ms6);
 int nomas_ffn_uses_mfma(const nomas_ffn_t *h);
 
 void nomas_ffn_destroy(nomas_ffn_t *h);
+
+/* ---- Block seams on their own ---------------------------------------------------
+ * The two expressions of DiTBlock::forward around its FFN (block.rs:96,101),
+ * for callers that run the FFN separately (the dense FeedForward of
+ * BlockFfn::Dense, block.rs:97-100).  Same conventions as
+ * nomas_moe_forward_block: (rows, dim) tensors in `dtype` on the device,
+ * 16-byte aligned, dim % 8 == 0, row r in sequence r / seq, f32 (rows / seq,
+ * dim) AdaLN parameters and f32 norm gain (16-byte aligned too), asynchronous
+ * on `stream` (of the current device). */
+
+/* h = modulate(norm2(x), shift, scale)  (block.rs:96; norm.rs:55-65,
+ * modulate.rs:69-79).  norm_w: norm2's gain as f32 or NULL (no_affine).
+ * h may alias x. */
+int nomas_norm_modulate(int dtype, const void *x, void *h, int64_t rows, int64_t dim, int64_t seq,
+                        const float *norm_w, double eps, const float *shift, const float *scale,
+                        void *stream);
+
+/* out = x + y * gate  (block.rs:101), y the FFN output; out may alias x or y. */
+int nomas_gated_residual(int dtype, const void *x, const void *y, const float *gate, void *out,
+                         int64_t rows, int64_t dim, int64_t seq, void *stream);
 
 /* Message of the last failure on this thread ("" if none). */
 const char *nomas_moe_last_error(void);

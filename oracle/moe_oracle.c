@@ -14,6 +14,10 @@
  *   nomas-core/src/modules/mod.rs:122-142   Lin::fwd  (x @ W^T + b, rows folded)
  *   nomas-core/src/modules/moe.rs:65-109    MoeLayer::forward
  *   nomas-core/src/modules/mlp.rs:39-48     FeedForward::SwiGlu (orc_ffn_f64, and each expert)
+ *   nomas-core/src/modules/norm.rs:55-65     RmsNorm::forward     (orc_norm_modulate)
+ *   nomas-core/src/modules/modulate.rs:69-79 modulate             (orc_norm_modulate)
+ *   nomas-core/src/modules/block.rs:96,101   the FFN seams of DiTBlock::forward
+ *                                            (orc_norm_modulate, orc_gated_residual)
  *
  * Two evaluation modes:
  *   - sparse f64  (orc_forward_sparse_f64): routing from f64 logits, only the
@@ -52,6 +56,10 @@ enum {
     MUT_DOWN_TRANSPOSED = 6,  /* down weight indexed (in, out) instead of (out, in) */
     MUT_FNV_PRIME = 7,        /* FNV-1a with a wrong multiplier                 */
     MUT_SPLITMIX_SHIFT = 8,   /* SplitMix64 first xor-shift 31 instead of 30    */
+    MUT_MODULATE_NO_ONE = 9,  /* modulate multiplies by scale, not 1 + scale    */
+    MUT_VAR_D_MINUS_1 = 10,   /* RMSNorm mean over D - 1 elements               */
+    MUT_NORM_NO_ROUND = 11,   /* norm output not rounded to the model dtype     */
+    MUT_UNGATED_RESIDUAL = 12 /* residual adds y without the gate               */
 };
 
 /* ------------------------------------------------------------------ */
@@ -479,6 +487,106 @@ int orc_forward_dense_f32(int64_t T, int64_t D, int64_t E, int64_t k, int64_t H,
     }
     free(logits); free(wts); free(G); free(U); free(Y);
     return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* Block seams: block.rs:96,101, norm.rs:55-65, modulate.rs:69-79      */
+/* ------------------------------------------------------------------ */
+
+/* f32 -> f16 round-to-nearest-even, widened back (candle's to_dtype(F16) goes
+ * through half::f16::from_f32).  Written from the definition: the result is a
+ * multiple of the f16 quantum at the value's binade (2^(e-10), and 2^-24 below
+ * the normal range), chosen by rint (ties to even in the default rounding
+ * mode); magnitudes that round past 65504 become infinity; NaN stays NaN. */
+static float round_f16_1(float v)
+{
+    if (isnan(v) || isinf(v) || v == 0.0f) return v;
+    int ex;
+    (void)frexpf(v, &ex);            /* |v| = m * 2^ex, m in [0.5, 1) */
+    int q = ex - 11;                  /* quantum 2^q of an 11-bit significand */
+    if (q < -24) q = -24;             /* subnormal f16: fixed quantum 2^-24 */
+    float r = ldexpf(rintf(ldexpf(v, -q)), q);
+    if (fabsf(r) > 65504.0f) r = copysignf(INFINITY, v);
+    return r;
+}
+
+void orc_round_f16(float *a, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i) a[i] = round_f16_1(a[i]);
+}
+
+/* dt: 0 f32 (no rounding), 1 bf16, 2 f16 (DataType, config.rs:30-39) */
+static float round_dt(float v, int dt)
+{
+    if (dt == 1) {
+        orc_round_bf16(&v, 1);
+        return v;
+    }
+    if (dt == 2) return round_f16_1(v);
+    return v;
+}
+
+/* h = modulate(norm2(x), shift, scale) for rows x D activations already in the
+ * model dtype (widened to f32); row r in sequence r / seq, shift and scale
+ * (rows / seq, D), norm_w (D) or NULL (RmsNorm::no_affine).  Each step is one
+ * candle-core 0.11.1 f32 op rounded to f32, in the reference's order:
+ *   norm.rs:58-65   sq = x.powf(2); ss = sum (one add at a time, ascending d);
+ *                   var = ss * f32(1/D) (mean_keepdim = sum * (1/D));
+ *                   t = var + f32(eps); inv = t.powf(-0.5);
+ *                   n = x * inv; n = n * w; n -> model dtype
+ *   modulate.rs:76-78  m = n * (scale + 1) + shift in f32; m -> model dtype
+ * pow_mode 0 calls libm powf as the reference's f32::powf does; pow_mode 1
+ * uses the correctly rounded forms (x*x, and 1/sqrt in double rounded once),
+ * which powf matches except where its result lands within its error bound of
+ * a rounding midpoint.  inv_out (rows) may be NULL. */
+void orc_norm_modulate(int64_t rows, int64_t D, int64_t seq, const float *x,
+                       const float *norm_w, double eps, const float *shift,
+                       const float *scale, int dt, int pow_mode, float *h, float *inv_out)
+{
+    volatile float two = 2.0f, mhalf = -0.5f; /* runtime exponents: no folding */
+    const float p2 = two, pm = mhalf;
+    const float inv_d = (float)(1.0 / (double)(orc_mutation == MUT_VAR_D_MINUS_1 ? D - 1 : D));
+    const float eps_f = (float)eps;
+    for (int64_t r = 0; r < rows; ++r) {
+        const float *xr = x + r * D;
+        float ss = 0.0f;
+        for (int64_t d = 0; d < D; ++d) {
+            const float sq = pow_mode ? xr[d] * xr[d] : powf(xr[d], p2);
+            ss = ss + sq;
+        }
+        const float var = ss * inv_d;
+        const float t = var + eps_f;
+        const float inv = pow_mode ? (float)(1.0 / sqrt((double)t)) : powf(t, pm);
+        if (inv_out) inv_out[r] = inv;
+        const int64_t b = r / seq;
+        const float *sc = scale + b * D, *sh = shift + b * D;
+        float *hr = h + r * D;
+        for (int64_t d = 0; d < D; ++d) {
+            float n = xr[d] * inv;
+            if (norm_w) n = n * norm_w[d];
+            if (orc_mutation != MUT_NORM_NO_ROUND) n = round_dt(n, dt);
+            const float opl = orc_mutation == MUT_MODULATE_NO_ONE ? sc[d] : sc[d] + 1.0f;
+            float m = n * opl;
+            m = m + sh[d];
+            hr[d] = round_dt(m, dt);
+        }
+    }
+}
+
+/* out = x + y * gate (block.rs:101): y is the FFN output in the model dtype,
+ * gate (rows / seq, D); the product and the sum each rounded to the model
+ * dtype, as tensor ops in that dtype do. */
+void orc_gated_residual(int64_t rows, int64_t D, int64_t seq, const float *x, const float *y,
+                        const float *gate, int dt, float *out)
+{
+    for (int64_t r = 0; r < rows; ++r) {
+        const float *g = gate + (r / seq) * D;
+        for (int64_t d = 0; d < D; ++d) {
+            const float t = round_dt(orc_mutation == MUT_UNGATED_RESIDUAL ? y[r * D + d]
+                                                                       : y[r * D + d] * g[d], dt);
+            out[r * D + d] = round_dt(x[r * D + d] + t, dt);
+        }
+    }
 }
 
 int orc_num_threads(void)

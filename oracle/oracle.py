@@ -3,8 +3,10 @@
 TEST INFRASTRUCTURE ONLY: imported by the tests, the smoke check and the
 CPU-baseline leg of ``bench.py``, never by the product package.  The C source
 (``moe_oracle.c``) restates hy-nomas-rs's generator (tensor_utils.rs:65-162,
-modules/mod.rs:47-55) and ``MoeLayer::forward`` (modules/moe.rs:65-109,
-modules/mlp.rs:42-46); this module only marshals numpy arrays.
+modules/mod.rs:47-55), ``MoeLayer::forward`` (modules/moe.rs:65-109,
+modules/mlp.rs:42-46) and the FFN seams of ``DiTBlock::forward``
+(modules/block.rs:96,101, modules/norm.rs:55-65, modules/modulate.rs:69-79);
+this module only marshals numpy arrays.
 """
 from __future__ import annotations
 
@@ -61,6 +63,13 @@ def lib():
     L.orc_forward_dense_f32.argtypes = (
         [C.c_int64] * 5 + [C.c_void_p] * 8 + [C.c_double] + [C.c_void_p] * 6
         + [_f32p, C.c_void_p])
+    L.orc_round_f16.restype = None
+    L.orc_round_f16.argtypes = [_f32p, C.c_int64]
+    L.orc_norm_modulate.restype = None
+    L.orc_norm_modulate.argtypes = ([C.c_int64] * 3 + [_f32p, C.c_void_p, C.c_double, _f32p, _f32p]
+                                    + [C.c_int, C.c_int, _f32p, _f32p])
+    L.orc_gated_residual.restype = None
+    L.orc_gated_residual.argtypes = [C.c_int64] * 3 + [_f32p] * 3 + [C.c_int, _f32p]
     L.orc_num_threads.restype = C.c_int
     L.orc_set_num_threads.restype = None
     L.orc_set_num_threads.argtypes = [C.c_int]
@@ -81,6 +90,10 @@ MUTATIONS = {
     "down_transposed": 6,
     "fnv_prime": 7,
     "splitmix_shift": 8,
+    "modulate_no_one": 9,
+    "var_d_minus_1": 10,
+    "norm_no_round": 11,
+    "ungated_residual": 12,
 }
 
 
@@ -123,6 +136,56 @@ def round_bf16(a: np.ndarray) -> np.ndarray:
     out = np.array(a, dtype=np.float32, copy=True, order="C")
     lib().orc_round_bf16(out, out.size)
     return out
+
+
+def round_f16(a: np.ndarray) -> np.ndarray:
+    out = np.array(a, dtype=np.float32, copy=True, order="C")
+    lib().orc_round_f16(out, out.size)
+    return out
+
+
+DT_CODE = {"f32": 0, "bf16": 1, "f16": 2}
+
+
+def round_dt(a: np.ndarray, dt: str) -> np.ndarray:
+    """Round f32 values to the model dtype, widened back to f32."""
+    return {"f32": lambda v: np.array(v, np.float32), "bf16": round_bf16, "f16": round_f16}[dt](a)
+
+
+def norm_modulate(x, shift, scale, seq, norm_w=None, eps=1e-6, dt="f32", pow_mode=0):
+    """h = modulate(norm2(x), shift, scale) (norm.rs:55-65, modulate.rs:69-79).
+
+    x: (rows, D) values of the model dtype (as f32); shift / scale (rows/seq, D).
+    Returns (h (rows, D) f32 holding model-dtype values, inv_rms (rows,)).
+    pow_mode 0: libm powf as the reference; 1: correctly rounded square and root.
+    """
+    x = _f32(x)
+    rows, D = x.shape
+    h = np.empty_like(x)
+    inv = np.empty(rows, np.float32)
+    nw = _f32(norm_w)
+    lib().orc_norm_modulate(rows, D, int(seq), x, _ptr(nw), float(eps), _f32(shift),
+                            _f32(scale), DT_CODE[dt], int(pow_mode), h, inv)
+    return h, inv
+
+
+def gated_residual(x, y, gate, seq, dt="f32"):
+    """out = x + y * gate (block.rs:101), each op rounded to the model dtype."""
+    x, y = _f32(x), _f32(y)
+    out = np.empty_like(x)
+    lib().orc_gated_residual(x.shape[0], x.shape[1], int(seq), x, y, _f32(gate), DT_CODE[dt], out)
+    return out
+
+
+def block_ffn(x, p, k, shift, scale, gate, seq, norm_w=None, eps=1e-6, dt="f32", pow_mode=0,
+              shared_dense=0.0, dense=None):
+    """The FFN half of DiTBlock::forward around the MoE (block.rs:96-101):
+    returns (out (rows, D) f32 in the model dtype, h, idx, gap), the MoE in f64
+    (forward_sparse) with its output rounded to the model dtype."""
+    h, _ = norm_modulate(x, shift, scale, seq, norm_w, eps, dt, pow_mode)
+    y, idx, _, gap = forward_sparse(h, p, k, shared_dense=shared_dense, dense=dense)
+    y_dt = round_dt(y.astype(np.float32), dt)
+    return gated_residual(x, y_dt, gate, seq, dt), h, idx, gap
 
 
 def route(x, wr, k):

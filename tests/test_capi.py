@@ -74,6 +74,24 @@ def test_null_arguments_are_rejected():
     L.nomas_moe_destroy(None)  # no-op
 
 
+def test_block_seam_arguments_are_checked_before_any_launch():
+    # block.rs:96,101 entry points: shapes, sequences, dtype and alignment are
+    # validated on the host (NOMAS_ERR_INVALID_ARGUMENT) -- no device needed
+    L = _lib.lib()
+    buf = (C.c_uint8 * 4096)()
+    a = (C.addressof(buf) + 15) // 16 * 16
+    assert L.nomas_norm_modulate(1, a, a, 10, 256, 3, None, 1e-6, a, a, None) == 2  # 10 % 3
+    assert b"sequences" in L.nomas_moe_last_error()
+    assert L.nomas_norm_modulate(1, a, a, 4, 252, 4, None, 1e-6, a, a, None) == 2   # dim % 8
+    assert L.nomas_norm_modulate(7, a, a, 4, 256, 4, None, 1e-6, a, a, None) == 2   # dtype
+    assert L.nomas_norm_modulate(1, a + 2, a, 4, 256, 4, None, 1e-6, a, a, None) == 2  # align
+    assert L.nomas_norm_modulate(1, a, a, 4, 256, 4, None, -1.0, a, a, None) == 2   # eps
+    assert L.nomas_norm_modulate(1, a, a, 4, 256, 4, None, 1e-6, a, None, None) == 2  # scale
+    assert L.nomas_gated_residual(1, a, a, None, a, 4, 256, 4, None) == 2            # gate
+    assert L.nomas_norm_modulate(1, None, None, 0, 256, 1, None, 1e-6, None, None, None) == 0
+    assert L.nomas_moe_forward_block(None, a, a, 4, 4, None, 1e-6, a, a, a, None) == 2
+
+
 def _checkpoint(path, E, D, H, dtype=np.float32, drop=(), reshape=None, dense=False):
     rng = np.random.default_rng(0)
     t = {"blocks.0.moe.router.weight": rng.standard_normal((E, D)).astype(dtype)}

@@ -296,13 +296,138 @@ def pin_ffn_equals_single_expert():
     np.testing.assert_allclose(O.ffn(x, f), moe * (1.0 + 1e-9), rtol=1e-12, atol=1e-14)
 
 
+# --------------------------------------------------------------------------
+# block seams: norm2 + modulate (norm.rs:55-65, modulate.rs:69-79) and the
+# gated residual (block.rs:101)
+# --------------------------------------------------------------------------
+
+def pin_f16_rounding():
+    # numpy's float16 cast is round-to-nearest-even with subnormals and overflow
+    rng = np.random.default_rng(8)
+    x = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.float32(2.0) ** rng.integers(
+            -30, 18, 20000).astype(np.float32),
+        np.array([0.0, -0.0, 65504.0, 65519.9, 65520.0, 1e6, -1e6, 2.0 ** -24, 2.0 ** -25,
+                  3 * 2.0 ** -26, 2.0 ** -14, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11,
+                  np.inf, -np.inf], np.float32)])
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).astype(np.float32)
+    np.testing.assert_array_equal(O.round_f16(x), want)
+    assert np.isnan(O.round_f16(np.array([np.nan], np.float32))).all()
+
+
+def pin_modulate_formula():
+    # the reference's modulate_formula test (modulate.rs:85-99): x = ones(1,3,4),
+    # shift [1,0,0,0], scale [0,1,0,0] -> token 0 [2,2,1,1], token 1 col 0 = 2.
+    # eps = 0 makes the norm of a row of ones exactly 1.
+    h, inv = O.norm_modulate(np.ones((3, 4), np.float32), np.array([[1, 0, 0, 0]], np.float32),
+                             np.array([[0, 1, 0, 0]], np.float32), seq=3, eps=0.0)
+    assert (inv == 1.0).all()
+    np.testing.assert_array_equal(h, np.tile(np.array([2, 2, 1, 1], np.float32), (3, 1)))
+
+
+def pin_rms_norm_unit_variance():
+    # norm.rs:80-92: RmsNorm::no_affine(16, 1e-6) on deterministic_randn([2,5,16], 7)
+    # gives rows of mean square 1 within 1e-3 (modulate with zero shift/scale is
+    # the identity)
+    x = O.randn_affine(7, 2 * 5 * 16).reshape(10, 16)
+    z = np.zeros((2, 16), np.float32)
+    h, _ = O.norm_modulate(x, z, z, seq=5, eps=1e-6)
+    ms = (h.astype(np.float64) ** 2).mean(axis=1)
+    assert np.abs(ms - 1.0).max() < 1e-3, ms
+
+
+def pin_zero_row_stays_finite():
+    # norm.rs:94-106: a zero row normalises to zeros (inv = eps^-1/2)
+    z = np.zeros((1, 8), np.float32)
+    sh = np.arange(8, dtype=np.float32)[None] * np.float32(0.25)
+    h, inv = O.norm_modulate(z, sh, np.ones((1, 8), np.float32), seq=1, eps=1e-6)
+    assert np.isfinite(h).all() and np.isfinite(inv).all()
+    np.testing.assert_array_equal(h, sh)  # 0 * (1 + 1) + shift
+    assert abs(inv[0] - 1000.0) <= 1e-3
+
+
+def _seam_case(seed, rows, D, seq):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((rows, D)).astype(np.float32) * np.float32(1.7)
+    nb = rows // seq
+    return (x, rng.standard_normal(D).astype(np.float32),
+            (rng.standard_normal((nb, D)) * 0.5).astype(np.float32),
+            (rng.standard_normal((nb, D)) * 0.5).astype(np.float32))
+
+
+def pin_norm_modulate_f32_vs_float64():
+    # f32 model: every step is an f32 op, so h is the exact f64 formula within a
+    # few f32 ulps (the sequential f32 sum of D squares is the largest term)
+    x, w, sh, sc = _seam_case(9, 12, 256, 4)
+    h, inv = O.norm_modulate(x, sh, sc, seq=4, norm_w=w, eps=1e-6, dt="f32")
+    xd = x.astype(np.float64)
+    inv_ref = 1.0 / np.sqrt((xd ** 2).mean(axis=1) + 1e-6)
+    np.testing.assert_allclose(inv, inv_ref, rtol=2e-6)
+    b = np.arange(12) // 4
+    ref = xd * inv_ref[:, None] * w * (1.0 + sc[b]) + sh[b]
+    np.testing.assert_allclose(h, ref, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
+
+
+def pin_norm_modulate_bf16_vs_torch():
+    # the same op sequence as torch bf16 tensor ops (torch's own reductions and
+    # roundings): elements agree bit for bit except where torch's differently
+    # ordered sum moves inv across a bf16 rounding edge (one ulp apart)
+    for dt, tdt in (("bf16", torch.bfloat16), ("f16", torch.float16)):
+        x, w, sh, sc = _seam_case(10, 64, 512, 16)
+        xt = torch.from_numpy(x).to(tdt)
+        xm = xt.float().numpy()
+        h, _ = O.norm_modulate(xm, sh, sc, seq=16, norm_w=w, eps=1e-6, dt=dt)
+        f = xt.float()
+        inv = (f.pow(2).mean(-1, keepdim=True) + 1e-6).pow(-0.5)
+        n = (f * inv * torch.from_numpy(w)).to(tdt).float()
+        b = torch.arange(64) // 16
+        opl = torch.from_numpy(sc)[b] + 1.0
+        m = (n * opl + torch.from_numpy(sh)[b]).to(tdt).float()
+        eq = (h == m.numpy()).mean()
+        # an ulp of n carried through (1 + scale), plus an ulp of h
+        u = 2.0 ** -7 if dt == "bf16" else 2.0 ** -10
+        bound = (u * ((n * opl).abs() + m.abs())).numpy()
+        assert eq >= 0.995 and (np.abs(h - m.numpy()) <= bound).all(), (dt, eq)
+
+
+def pin_pow_modes_agree():
+    # libm powf against correctly rounded square / root: the same bits except
+    # where powf's result lands within its error bound of a midpoint
+    x, w, sh, sc = _seam_case(11, 200, 384, 50)
+    for dt in ("f32", "bf16"):
+        xm = O.round_dt(x, dt)
+        h0, i0 = O.norm_modulate(xm, sh, sc, 50, w, 1e-6, dt, pow_mode=0)
+        h1, i1 = O.norm_modulate(xm, sh, sc, 50, w, 1e-6, dt, pow_mode=1)
+        assert (i0 == i1).mean() >= 0.99
+        assert (np.abs(i0.view(np.int32) - i1.view(np.int32)) <= 1).all()
+
+
+def pin_gated_residual_closed_forms():
+    rng = np.random.default_rng(12)
+    for dt, tdt in (("f32", torch.float32), ("bf16", torch.bfloat16), ("f16", torch.float16)):
+        x = O.round_dt(rng.standard_normal((6, 32)).astype(np.float32), dt)
+        y = O.round_dt(rng.standard_normal((6, 32)).astype(np.float32), dt)
+        zero, one = np.zeros((2, 32), np.float32), np.ones((2, 32), np.float32)
+        np.testing.assert_array_equal(O.gated_residual(x, y, zero, 3, dt), x)
+        # gate 1: the model dtype's own addition
+        want = (torch.from_numpy(x).to(tdt) + torch.from_numpy(y).to(tdt)).float().numpy()
+        np.testing.assert_array_equal(O.gated_residual(x, y, one, 3, dt), want)
+        # gate 2: doubling is exact, so x + 2y rounds once
+        want2 = (torch.from_numpy(x).to(tdt) + 2 * torch.from_numpy(y).to(tdt)).float().numpy()
+        np.testing.assert_array_equal(O.gated_residual(x, y, 2 * one, 3, dt), want2)
+
+
 PINS = [pin_splitmix64, pin_fnv1a, pin_box_muller, pin_affine_and_moments, pin_uniform,
         pin_xavier_std,
         pin_bf16_rounding, pin_route_bruteforce, pin_route_ties_lowest_index,
         pin_route_one_hot_rows, pin_route_weights_sum_to_one, pin_forward_bruteforce,
         pin_dense_equals_sparse, pin_k_equals_experts, pin_single_dominant_expert,
         pin_zero_input_zero_output, pin_row_permutation, pin_shared_dense_branch,
-        pin_ffn_bruteforce, pin_ffn_equals_single_expert]
+        pin_ffn_bruteforce, pin_ffn_equals_single_expert,
+        pin_f16_rounding, pin_modulate_formula, pin_rms_norm_unit_variance,
+        pin_zero_row_stays_finite, pin_norm_modulate_f32_vs_float64,
+        pin_norm_modulate_bf16_vs_torch, pin_pow_modes_agree, pin_gated_residual_closed_forms]
 
 
 @pytest.mark.parametrize("pin", PINS, ids=[p.__name__ for p in PINS])
