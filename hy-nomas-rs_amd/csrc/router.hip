@@ -2,10 +2,12 @@
 // one kernel (hy-nomas-rs moe.rs:67-95).
 //
 // One block = 16 waves = one chunk of 64 rows.
-//  - Logits are f64 matrix products (v_mfma_f64_16x16x4_f64).  A product of
-//    two bf16/f16 or two f32 inputs is exact in f64, so the only rounding is
-//    the f64 summation (relative 1e-16): expert choice is decided far below
-//    the 1e-6 logit near-tie threshold, as by an exact evaluation.
+//  - Logits.  bf16/f16 inputs: one v_mfma_f32_16x16x32 per 32 k (products
+//    exact in f32, 32 of them summed in f32), the per-MFMA sums added in f64
+//    in k order; the logit error is a few f32 ulps of a 32-term partial sum
+//    (~1e-8 on unit-scale logits).  f32 inputs: f64 matrix products
+//    (v_mfma_f64_16x16x4_f64, exact products, f64 sums).  Either way expert
+//    choice is decided far below the 1e-6 logit near-tie threshold.
 //  - Wave (g, q) computes rows 16g..16g+15 of the chunk against 16 experts at
 //    a time over the q-th quarter of D; the four quarters are added in a fixed
 //    order (q = 0, 1, 2, 3) through LDS, so results do not depend on timing.
@@ -13,9 +15,11 @@
 //    weights) per step and feeds them to consecutive MFMAs: the k index of
 //    MFMA i, lane group lg is k0 + lg * EPC + i, the same assignment for both
 //    operands, so the 4-deep MFMA k dimension reads whole 16-byte chunks.
-//  - Selection is wave-parallel over experts: max / sum / k rounds of argmax
-//    are xor-shuffle reductions across the wave.  Ties go to the lowest
-//    expert index, the reference's first-max-wins argmax (moe.rs:78-80).
+//  - Selection: with E <= 64 four lanes take a row (a quarter of its experts
+//    each, combined by two xor shuffles; waves 0-3, one per SIMD); with more
+//    experts it is wave-parallel over experts (max / sum / k rounds of argmax
+//    as xor-shuffle reductions across the wave).  Ties go to the
+//    lowest expert index, the reference's first-max-wins argmax (moe.rs:78-80).
 //  - Gates: p = exp(l - max) / sum_E exp(l - max), w = p / (sum_selected p + 1e-9)
 //    (moe.rs:68,92-95), evaluated in f64 and stored as f32.
 //  - Output per row: k experts in ascending index with their gates, the
@@ -38,6 +42,35 @@ static_assert(kGroups * 16 == kRouterRows, "4 groups of 16 rows per chunk");
 static_assert(kGroups * kParts * kWave == kRouterThreads, "one wave per (group, part)");
 
 typedef double d4 __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+// v_mfma_f32_16x16x32_{bf16,f16} on raw 16-byte operands, C = 0: lane l gives
+// row l % 16 of A (x) and column l % 16 of B (weights) at k 8 (l / 16) .. +7;
+// the result lane l holds C[4 (l / 16) + r][l % 16], r = 0..3.
+template <typename T> struct Mfma16;
+template <> struct Mfma16<__bf16> {
+    static __device__ __forceinline__ f32x4_t run(const uint4& a, const uint4& b) {
+        bf16x8_t av, bv;
+        __builtin_memcpy(&av, &a, 16);
+        __builtin_memcpy(&bv, &b, 16);
+        const f32x4_t z = {0.0f, 0.0f, 0.0f, 0.0f};
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, z, 0, 0, 0);
+    }
+};
+template <> struct Mfma16<_Float16> {
+    static __device__ __forceinline__ f32x4_t run(const uint4& a, const uint4& b) {
+        f16x8_t av, bv;
+        __builtin_memcpy(&av, &a, 16);
+        __builtin_memcpy(&bv, &b, 16);
+        const f32x4_t z = {0.0f, 0.0f, 0.0f, 0.0f};
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, z, 0, 0, 0);
+    }
+};
+template <> struct Mfma16<float> {  // not used: f32 inputs take the f64 MFMAs
+    static __device__ __forceinline__ f32x4_t run(const uint4&, const uint4&) { return {}; }
+};
 
 __device__ __forceinline__ double wave_max(double v) {
 #pragma unroll
@@ -94,36 +127,55 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
         const int ex = e0 + r16;
         const bool ex_ok = ex < E;
         const T* wrr = wr + (int64_t)(ex_ok ? ex : 0) * D;
+        // Loads are unconditional from clamped addresses (a load whose address
+        // or value is chosen by a condition becomes a flat load with a
+        // scratch-resident zero); chunks past this part's steps or past D are
+        // zeroed where they are used.  Rows past the end and experts past E
+        // read row 0 / expert 0: their logits are never used.
         auto fetch = [&](int st, uint4& xa, uint4& wa) {
-            const int kk = st * CK + lg * EPC;  // D % 8 == 0: a chunk is wholly in or out
-            const uint4 z = make_uint4(0, 0, 0, 0);
-            xa = (st < s1 && row_ok && kk < D) ? *reinterpret_cast<const uint4*>(xr + kk) : z;
-            wa = (st < s1 && ex_ok && kk < D) ? *reinterpret_cast<const uint4*>(wrr + kk) : z;
+            const int kk = min(max(min(st, s1 - 1), 0) * CK + lg * EPC, D - EPC);
+            xa = *reinterpret_cast<const uint4*>(xr + kk);
+            wa = *reinterpret_cast<const uint4*>(wrr + kk);
         };
+        auto live = [&](int st) { return st < s1 && st * CK + lg * EPC < D; };  // D % 8 == 0
         uint4 xb[kPre], wb[kPre];
 #pragma unroll
         for (int p = 0; p < kPre; ++p) fetch(s0 + p, xb[p], wb[p]);
         d4 c0 = {0.0, 0.0, 0.0, 0.0}, c1 = {0.0, 0.0, 0.0, 0.0};
-        // whole turns of the ring: steps past s1 hold zeros, which add exactly 0
+        // whole turns of the ring: steps past s1 are zeroed, which adds exactly 0
         for (int st0 = s0; st0 < s1; st0 += kPre) {
 #pragma unroll
             for (int p = 0; p < kPre; ++p) {
+                if (!live(st0 + p)) {
+                    xb[p] = make_uint4(0, 0, 0, 0);
+                    wb[p] = make_uint4(0, 0, 0, 0);
+                }
+                if constexpr (sizeof(T) == 2) {
+                    // one 16x16x32 MFMA per step: the 32 products are exact in
+                    // f32 and summed there; each step's sums join the f64
+                    // accumulators in step order
+                    const f32x4_t m = Mfma16<T>::run(xb[p], wb[p]);
 #pragma unroll
-                for (int i = 0; i < EPC; ++i) {
-                    const double xd = unpack(xb[p], i), wd = unpack(wb[p], i);
-                    if (i & 1) c1 = __builtin_amdgcn_mfma_f64_16x16x4f64(xd, wd, c1, 0, 0, 0);
-                    else c0 = __builtin_amdgcn_mfma_f64_16x16x4f64(xd, wd, c0, 0, 0, 0);
+                    for (int r = 0; r < 4; ++r) c0[r] += (double)m[r];
+                } else {
+#pragma unroll
+                    for (int i = 0; i < EPC; ++i) {
+                        const double xd = unpack(xb[p], i), wd = unpack(wb[p], i);
+                        if (i & 1) c1 = __builtin_amdgcn_mfma_f64_16x16x4f64(xd, wd, c1, 0, 0, 0);
+                        else c0 = __builtin_amdgcn_mfma_f64_16x16x4f64(xd, wd, c0, 0, 0, 0);
+                    }
                 }
                 fetch(st0 + p + kPre, xb[p], wb[p]);
             }
         }
         const d4 c = c0 + c1;
-        // lane holds rows lg + 4 r (r = 0..3) of the group, expert column r16;
-        // part 0 writes the logit slots, parts 1..3 their own buffers
+        // lane holds expert column r16 of rows 4 lg + r (16-bit inputs) or
+        // lg + 4 r (f32) of the group; part 0 writes the logit slots, parts
+        // 1..3 their own buffers
         __syncthreads();  // the previous block's reads of s_part are done
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int i = lg + 4 * r;
+            const int i = sizeof(T) == 2 ? 4 * lg + r : lg + 4 * r;
             if (q == 0) {
                 if (ex_ok) s_logit[(g * 16 + i) * E + ex] = c[r];
             } else {
@@ -144,6 +196,76 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
     }
     __syncthreads();
 
+    if (E <= kWave) {
+        // Four lanes per row (waves 0-3, one per SIMD): lane sub of a row's
+        // quad takes experts sub, sub + 4, ...; max, sums and argmax combine
+        // over the quad with two xor shuffles.
+        if (wave < 4) {
+            const int lr = tid >> 2, sub = tid & 3;
+            const int64_t orow = chunk_row0 + lr;
+            const bool ok = orow < rows;  // lanes of missing rows still shuffle
+            const double* lgt = s_logit + (ok ? lr : 0) * E;
+            auto quad_max = [](double v) {
+                v = fmax(v, __shfl_xor(v, 1));
+                return fmax(v, __shfl_xor(v, 2));
+            };
+            auto quad_sum = [](double v) {
+                v += __shfl_xor(v, 1);
+                return v + __shfl_xor(v, 2);
+            };
+            double m = -INFINITY;
+            for (int e = sub; e < E; e += 4) m = fmax(m, lgt[e]);
+            m = quad_max(m);
+            double s = 0.0;
+            for (int e = sub; e < E; e += 4) s += exp(lgt[e] - m);
+            s = quad_sum(s);
+            uint64_t sel = 0;  // all selected experts of the row (every lane of the quad)
+            double kth = INFINITY;
+            for (int it = 0; it < k; ++it) {
+                double bv = 0.0;
+                int bi = -1;
+                for (int e = sub; e < E; e += 4)
+                    if (!((sel >> e) & 1ull) && (bi < 0 || lgt[e] > bv)) { bv = lgt[e]; bi = e; }
+#pragma unroll
+                for (int o = 1; o <= 2; o <<= 1) {  // first maximum wins: lowest index
+                    const double ov = __shfl_xor(bv, o);
+                    const int oi = __shfl_xor(bi, o);
+                    if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
+                }
+                sel |= 1ull << bi;
+                kth = bv;
+            }
+            double best_un = -INFINITY, psel = 0.0;
+            for (int e = sub; e < E; e += 4) {
+                if ((sel >> e) & 1ull) psel += exp(lgt[e] - m) / s;
+                else best_un = fmax(best_un, lgt[e]);
+            }
+            best_un = quad_max(best_un);
+            psel = quad_sum(psel);
+            if (ok) {
+                for (int e = sub; e < E; e += 4) {
+                    if (!((sel >> e) & 1ull)) continue;
+                    const int rank = __popcll(sel & ((1ull << e) - 1ull));  // ascending index
+                    const double p = exp(lgt[e] - m) / s;
+                    topk_idx[orow * k_slots + rank] = e;
+                    topk_w[orow * k_slots + rank] = (float)(p / (psel + 1e-9));
+                    atomicAdd(&s_cnt[e], 1);
+                }
+                if (sub == 0) {
+                    gap[orow] = (k == E) ? INFINITY : (float)(kth - best_un);
+                    if (k_slots > k) {
+                        topk_idx[orow * k_slots + k] = E;
+                        topk_w[orow * k_slots + k] = dense_coef;
+                        atomicAdd(&s_cnt[E], 1);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        for (int e = tid; e < E_cols; e += kRouterThreads)
+            chunk_counts[(int64_t)blockIdx.x * E_cols + e] = s_cnt[e];
+        return;
+    }
     const int per_lane = (E + kWave - 1) / kWave;  // experts per lane (<= 4 for E <= 256)
     for (int r = 0; r < kRowsPerWave; ++r) {
         const int lr = wave * kRowsPerWave + r;
