@@ -16,211 +16,304 @@ namespace nomas {
 
 namespace {
 
-constexpr int kScanThreads = 1024;
+constexpr int kDispThreads = 1024;
+constexpr int kDispWaves = kDispThreads / kWave;
+constexpr int kSlabBytes = 512;                // bytes of a row per slab
+constexpr int kSlabStride = kSlabBytes + 16;   // LDS row, padded
+constexpr int kSlabPieces = kSlabBytes / 16;   // 16-byte pieces per row per slab
+constexpr int kProdThreads = kDispThreads / 2; // waves 0-7 load, waves 8-15 store
+constexpr int kProdLoads = kRouterRows * kSlabPieces / kProdThreads;  // 4
+static_assert(kProdLoads * kProdThreads == kRouterRows * kSlabPieces, "whole slabs");
 
-// Exclusive scan of one int per thread across the block (1024 threads).
-// Returns the exclusive prefix; *total receives the block sum.
-__device__ int block_exclusive_scan(int v, int* s_wave, int* total) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    int incl = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int t = __shfl_up(incl, o);
-        if (lane >= o) incl += t;
-    }
-    if (lane == 63) s_wave[wave] = incl;
-    __syncthreads();
-    if (wave == 0) {
-        int w = lane < kScanThreads / 64 ? s_wave[lane] : 0;
-        int wi = w;
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) {
-            const int t = __shfl_up(wi, o);
-            if (lane >= o) wi += t;
-        }
-        if (lane < kScanThreads / 64) s_wave[16 + lane] = wi - w;
-        if (lane == kScanThreads / 64 - 1) s_wave[32] = wi;
-    }
-    __syncthreads();
-    const int excl = incl - v + s_wave[16 + wave];
-    *total = s_wave[32];
-    __syncthreads();
-    return excl;
+// LDS of dispatch_kernel: two slabs (which first hold the histogram partials
+// and the chunk's expert slots), then the int arrays that live to the end.
+constexpr size_t kSlabLds = (size_t)2 * kRouterRows * kSlabStride;
+__host__ __device__ inline size_t dispatch_lds(int E_cols, int k) {
+    return kSlabLds + sizeof(int) * ((size_t)4 * (E_cols + 1) + (size_t)2 * kRouterRows * k);
+}
+__host__ __device__ inline bool dispatch_fits(int E_cols, int k) {
+    return sizeof(int) * ((size_t)2 * kDispWaves * E_cols + (size_t)kRouterRows * k) <= kSlabLds &&
+           dispatch_lds(E_cols, k) <= 160 * 1024;
 }
 
-// Single block.  From the per-chunk expert histograms computes
-//  - chunk_base[c][e]: first position of chunk c's rows of expert e,
-//  - expert_count[e], expert_off[e] (exclusive scan, expert_off[E] = A),
-//  - the GEMM tile table: ceil(count_e / BM) tiles of BM rows per expert.
-// Each thread owns one (expert, slice of chunks) pair so the serial work is
-// about sqrt(nchunks) per thread.
-__global__ __launch_bounds__(kScanThreads) void scan_kernel(ScanArgs a) {
-    __shared__ int s_part[kScanThreads];
-    __shared__ int s_tot[kMaxExperts + 1];
-    __shared__ int s_off[kMaxExperts + 1];
-    __shared__ int s_tstart[kMaxExperts + 1];
-    __shared__ int s_wave[40];
-    const int tid = threadIdx.x;
-    const int E = a.E_cols, nch = a.nchunks;
-    int nsl = 1;
-    while ((nsl * 2) * (nsl * 2) <= nch && (nsl * 2) * E <= kScanThreads) nsl *= 2;
-    const int cps = (nch + nsl - 1) / nsl;
-    const int e = tid % E, sl = tid / E;
-    const bool active = sl < nsl;
-    const int c0 = sl * cps, c1 = min(nch, c0 + cps);
-    int sum = 0;
-    if (active)
-        for (int c = c0; c < c1; ++c) sum += a.chunk_counts[(int64_t)c * E + e];
-    if (active) s_part[sl * E + e] = sum;
-    __syncthreads();
-    if (tid < E) {
-        int run = 0;
-        for (int q = 0; q < nsl; ++q) {
-            const int v = s_part[q * E + tid];
-            s_part[q * E + tid] = run;
-            run += v;
-        }
-        s_tot[tid] = run;
-    }
-    __syncthreads();
-    int total_rows;
-    const int ex = block_exclusive_scan(tid < E ? s_tot[tid] : 0, s_wave, &total_rows);
-    if (tid < E) s_off[tid] = ex;
-    __syncthreads();
-    if (active) {
-        int run = s_off[e] + s_part[sl * E + e];
-        for (int c = c0; c < c1; ++c) {
-            const int64_t i = (int64_t)c * E + e;
-            a.chunk_base[i] = run;
-            run += a.chunk_counts[i];
-        }
-    }
-    const int nt = tid < E ? (s_tot[tid] + a.BM - 1) / a.BM : 0;
-    int total_tiles;
-    const int ts = block_exclusive_scan(nt, s_wave, &total_tiles);
-    if (tid < E) {
-        s_tstart[tid] = ts;
-        a.expert_count[tid] = s_tot[tid];
-        a.expert_off[tid] = s_off[tid];
-    }
-    if (tid == 0) {
-        a.expert_off[E] = total_rows;
-        a.tile_total[0] = min(total_tiles, a.max_tiles);
-    }
-    __syncthreads();
-    for (int i = tid; i < total_tiles && i < a.max_tiles; i += kScanThreads) {
-        int lo = 0, hi = E - 1;  // last expert with tstart <= i (skipping empty ones)
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (s_tstart[mid] <= i) lo = mid; else hi = mid - 1;
-        }
-        while (lo > 0 && s_tstart[lo] > i) --lo;
-        const int j = i - s_tstart[lo];
-        TileInfo t;
-        t.expert = lo;
-        t.row0 = s_off[lo] + j * a.BM;
-        t.rows = min(a.BM, s_tot[lo] - j * a.BM);
-        t.pad = 0;
-        a.tiles[i] = t;
-    }
-}
-
-// One block per 64-row chunk.  Wave 0 ranks the chunk's slots: for each
-// expert in ascending order, a ballot over the 64 rows gives every row its
-// rank among the chunk's rows of that expert; adding the chunk base gives a
-// stable position.  Then all 16 waves copy rows: each x row is read once and
-// written to its k positions with 16-byte accesses.
+// One block per 64-row chunk.  It does the whole bookkeeping of its chunk
+// from the router's per-chunk histograms -- no separate scan pass:
+//  1. rows of each expert in the chunks before it and in all chunks (each
+//     wave sums every 16th chunk, the waves' partials added in LDS);
+//  2. expert offsets (exclusive scan over experts, ascending) and the chunk's
+//     own per-expert slot offsets; block 0 also publishes the expert counts
+//     and offsets and the GEMM tile table (ceil(count / BM) tiles of BM rows
+//     per expert);
+//  3. wave 0 ranks the chunk's slots: for each expert in ascending order, a
+//     ballot over the 64 rows gives every row its rank among the chunk's rows
+//     of that expert; base + rank is a stable position.  The slots are listed
+//     in position order (expert, then row), positions increasing;
+//  4. the copy, 512-byte column slabs of the 64 rows at a time: waves 0-7
+//     stream slabs of x into one half of an LDS double buffer, waves 8-15 write
+//     the other half to x_perm in position order, so consecutive lanes write
+//     consecutive positions: K-blocked, one run of (slots of an expert) x 64
+//     bytes per K-block; row-major, whole 512-byte slab rows.  Producers and
+//     consumers run separate loops with the same barriers, so neither waits
+//     on the other's memory operations.
 template <typename T>
-__global__ __launch_bounds__(1024) void dispatch_kernel(DispatchArgs a) {
-    extern __shared__ int s_dyn[];
-    const int k = a.k_slots;
-    int* s_idx = s_dyn;           // 64 x k
-    int* s_pos = s_dyn + 64 * k;  // 64 x k
-    const int tid = threadIdx.x;
-    const int64_t row0 = (int64_t)blockIdx.x * kRouterRows;
+__global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) {
+    extern __shared__ __align__(16) unsigned char s_raw[];
+    const int Ec = a.E_cols, k = a.k_slots, nch = a.nchunks, b = blockIdx.x;
+    unsigned char* slab = s_raw;                   // [2][64][kSlabStride] (step 4)
+    int* s_red = reinterpret_cast<int*>(s_raw);    // [2][16][Ec] (steps 1-2)
+    int* s_idx = s_red + 2 * kDispWaves * Ec;      // [64 k] the chunk's expert slots (steps 1-3)
+    int* s_bef = reinterpret_cast<int*>(s_raw + kSlabLds);  // [Ec + 1]
+    int* s_off = s_bef + Ec + 1;               // [Ec + 1]
+    int* s_lb = s_off + Ec + 1;                // [Ec + 1] the chunk's slots before expert e
+    int* s_ts = s_lb + Ec + 1;                 // [Ec + 1] first tile of expert e
+    int* s_prow = s_ts + Ec + 1;               // [64 k] row of the i-th slot in position order
+    int* s_ppos = s_prow + kRouterRows * k;    // [64 k] its position
+    int* s_tot = s_red;                        // [Ec] after the reduction (s_red is free)
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int64_t row0 = (int64_t)b * kRouterRows;
     const int nvalid = (int)min<int64_t>(kRouterRows, a.rows - row0);
-    for (int i = tid; i < 64 * k; i += 1024) {
+
+    // 1. histograms
+    for (int e = lane; e < Ec; e += kWave) {
+        int bef = 0, tot = 0;
+        for (int c = wave; c < nch; c += kDispWaves) {
+            const int v = a.chunk_counts[(int64_t)c * Ec + e];
+            tot += v;
+            bef += c < b ? v : 0;
+        }
+        s_red[wave * Ec + e] = bef;
+        s_red[(kDispWaves + wave) * Ec + e] = tot;
+    }
+    for (int i = tid; i < kRouterRows * k; i += kDispThreads)
         s_idx[i] = (i / k < nvalid) ? a.topk_idx[row0 * k + i] : -1;
-        s_pos[i] = -1;
+    __syncthreads();
+    int my_tot = 0;
+    if (tid < Ec) {
+        int bef = 0;
+        for (int w = 0; w < kDispWaves; ++w) {
+            bef += s_red[w * Ec + tid];
+            my_tot += s_red[(kDispWaves + w) * Ec + tid];
+        }
+        s_bef[tid] = bef;
     }
     __syncthreads();
-    if (tid < 64) {
-        const int lane = tid;
+    if (tid < Ec) s_tot[tid] = my_tot;
+    __syncthreads();
+    // 2. offsets: wave 0 scans 64 experts at a time with carries
+    if (wave == 0) {
+        int carry = 0, lcarry = 0, tcarry = 0;
+        for (int e0 = 0; e0 < Ec; e0 += kWave) {
+            const int e = e0 + lane;
+            const int v = e < Ec ? s_tot[e] : 0;
+            const int lv = e < Ec ? a.chunk_counts[(int64_t)b * Ec + e] : 0;
+            const int tv = (v + a.BM - 1) / a.BM;
+            int inc = v, linc = lv, tinc = tv;
+#pragma unroll
+            for (int o = 1; o < kWave; o <<= 1) {
+                const int t0 = __shfl_up(inc, o), t1 = __shfl_up(linc, o), t2 = __shfl_up(tinc, o);
+                if (lane >= o) {
+                    inc += t0;
+                    linc += t1;
+                    tinc += t2;
+                }
+            }
+            if (e < Ec) {
+                s_off[e] = carry + inc - v;
+                s_lb[e] = lcarry + linc - lv;
+                s_ts[e] = tcarry + tinc - tv;
+            }
+            carry += __shfl(inc, kWave - 1);
+            lcarry += __shfl(linc, kWave - 1);
+            tcarry += __shfl(tinc, kWave - 1);
+        }
+        if (lane == 0) {
+            s_off[Ec] = carry;
+            s_lb[Ec] = lcarry;
+            s_ts[Ec] = tcarry;
+        }
+    }
+    __syncthreads();
+    if (b == 0) {
+        for (int e = tid; e < Ec; e += kDispThreads) {
+            a.expert_count[e] = s_tot[e];
+            a.expert_off[e] = s_off[e];
+        }
+        const int total_tiles = s_ts[Ec];
+        if (tid == 0) {
+            a.expert_off[Ec] = s_off[Ec];
+            a.tile_total[0] = min(total_tiles, a.max_tiles);
+        }
+        for (int i = tid; i < total_tiles && i < a.max_tiles; i += kDispThreads) {
+            int lo = 0, hi = Ec - 1;  // last expert with s_ts <= i (skipping empty ones)
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (s_ts[mid] <= i) lo = mid; else hi = mid - 1;
+            }
+            const int j = i - s_ts[lo];
+            TileInfo t;
+            t.expert = lo;
+            t.row0 = s_off[lo] + j * a.BM;
+            t.rows = min(a.BM, s_tot[lo] - j * a.BM);
+            t.pad = 0;
+            a.tiles[i] = t;
+        }
+    }
+    // 3. ranks and positions
+    if (wave == 0) {
         const int* mine = s_idx + lane * k;
-        const int32_t* base = a.chunk_base + (int64_t)blockIdx.x * a.E_cols;
         int cur = 0;
-        for (int e = 0; e < a.E_cols; ++e) {
+        for (int e = 0; e < Ec; ++e) {
             const bool has = cur < k && mine[cur] == e;
             const uint64_t bal = __ballot(has);
             if (has) {
-                const int p = base[e] + __popcll(bal & ((1ull << lane) - 1ull));
-                s_pos[lane * k + cur] = p;
+                const int rank = __popcll(bal & ((1ull << lane) - 1ull));
+                const int p = s_off[e] + s_bef[e] + rank;
+                const int li = s_lb[e] + rank;
+                s_prow[li] = lane;
+                s_ppos[li] = p;
                 a.tok_pos[(row0 + lane) * k + cur] = p;
                 ++cur;
             }
         }
     }
     __syncthreads();
+    // 4. the copy
     constexpr int EPC = 16 / sizeof(T);
-    const int nchunk = a.D / EPC;
-    const int wave = tid >> 6, lane = tid & 63;
-    const T* x = static_cast<const T*>(a.x);
-    T* xp = static_cast<T*>(a.x_perm);
-    for (int r = wave * 4; r < wave * 4 + 4 && r < nvalid; ++r) {
-        const T* src = x + (row0 + r) * (int64_t)a.D;
-        for (int c = lane; c < nchunk; c += kWave) {
-            const uint4 v = *reinterpret_cast<const uint4*>(src + (int64_t)c * EPC);
-            const int64_t col = (int64_t)c * EPC;
-            for (int j = 0; j < k; ++j) {
-                const int p = s_pos[r * k + j];
-                if (p < 0 || p >= a.a_cap) continue;
-                // row-major (p, col) or K-blocked ((col / 32) * a_cap + p) * 32 + col % 32
+    constexpr int kPPK = kKBlock * (int)sizeof(T) / 16;  // pieces of one row in one K-block
+    static_assert(kSlabPieces % kPPK == 0, "a slab holds whole K-blocks");
+    const int nck = a.D / EPC;  // 16-byte chunks per row (D % 8 == 0)
+    const int nslab = (nck + kSlabPieces - 1) / kSlabPieces;
+    const int npairs = s_lb[Ec];
+    const T* __restrict__ x = static_cast<const T*>(a.x);  // x_perm is the layer's own buffer
+    T* __restrict__ xp = static_cast<T*>(a.x_perm);
+    if (tid < kProdThreads) {
+        // producers: slab sl + 1 into LDS while the consumers write slab sl;
+        // four 16-byte pieces per thread, in named registers
+        static_assert(kProdLoads == 4, "four pieces per producer thread");
+        auto fetch = [&](int sl, int u) {  // unconditional: clamped to a valid chunk
+            const int q = tid + u * kProdThreads;
+            const int r = min(q / kSlabPieces, nvalid - 1);
+            const int c = min(sl * kSlabPieces + q % kSlabPieces, nck - 1);
+            return *reinterpret_cast<const uint4*>(x + (row0 + r) * (int64_t)a.D + (int64_t)c * EPC);
+        };
+        auto stash = [&](int buf, int u, const uint4& v) {
+            const int q = tid + u * kProdThreads;
+            *reinterpret_cast<uint4*>(slab + (buf * kRouterRows + q / kSlabPieces) * kSlabStride +
+                                      (q % kSlabPieces) * 16) = v;
+        };
+        uint4 v0 = fetch(0, 0), v1 = fetch(0, 1), v2 = fetch(0, 2), v3 = fetch(0, 3);
+        stash(0, 0, v0);
+        stash(0, 1, v1);
+        stash(0, 2, v2);
+        stash(0, 3, v3);
+        v0 = fetch(1, 0);
+        v1 = fetch(1, 1);
+        v2 = fetch(1, 2);
+        v3 = fetch(1, 3);
+        __syncthreads();
+        for (int sl = 0; sl < nslab; ++sl) {
+            const int buf = (sl + 1) & 1;  // slabs past the end are never read
+            stash(buf, 0, v0);
+            stash(buf, 1, v1);
+            stash(buf, 2, v2);
+            stash(buf, 3, v3);
+            v0 = fetch(sl + 2, 0);
+            v1 = fetch(sl + 2, 1);
+            v2 = fetch(sl + 2, 2);
+            v3 = fetch(sl + 2, 3);
+            __syncthreads();
+        }
+    } else {
+        // consumers
+        const int ct = tid - kProdThreads;
+        const int npieces = npairs * kSlabPieces;
+        __syncthreads();
+        for (int sl = 0; sl < nslab; ++sl) {
+            const unsigned char* sb = slab + (sl & 1) * kRouterRows * kSlabStride;
+            for (int v = ct; v < npieces; v += kDispThreads - kProdThreads) {
+                int pr, h;
+                if (a.kblocked) {  // (K-block, slot, piece): runs along positions
+                    const int per_kb = npairs * kPPK;
+                    const int kbl = v / per_kb, rem = v - kbl * per_kb;
+                    pr = rem / kPPK;
+                    h = kbl * kPPK + rem % kPPK;
+                } else {  // (slot, piece): whole slab rows
+                    pr = v / kSlabPieces;
+                    h = v % kSlabPieces;
+                }
+                const int c = sl * kSlabPieces + h;
+                const int p = s_ppos[pr];
+                if (c >= nck || p < 0 || p >= a.a_cap) continue;
+                const uint4 val = *reinterpret_cast<const uint4*>(sb + s_prow[pr] * kSlabStride + h * 16);
+                const int64_t col = (int64_t)c * EPC;
                 const int64_t off = a.kblocked
                     ? ((col / kKBlock) * a.a_cap + p) * kKBlock + col % kKBlock
                     : (int64_t)p * a.D + col;
-                *reinterpret_cast<uint4*>(xp + off) = v;
+                *reinterpret_cast<uint4*>(xp + off) = val;
             }
+            __syncthreads();
         }
     }
 }
 
 // One wave per row: out[row] = sum_j w_j * y_perm[pos_j] over the row's slots
-// in ascending expert order (then the dense slot), accumulated in f32.
+// in ascending expert order (then the dense slot), accumulated in f32.  The
+// row's positions and gates are read once (lane j holds slot j) and broadcast
+// with readlane; each lane then has its chunks' k loads in flight together.
 template <typename T>
 __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + wave;
     if (row >= a.rows) return;
     constexpr int EPC = 16 / sizeof(T);
+    constexpr int kBatch = 2;  // chunks per lane in flight
     const int nchunk = a.D / EPC;
-    const int k = a.k_slots;
-    const T* y = static_cast<const T*>(a.y_perm);
+    const int k = a.k_slots;   // slots past 64 are read from memory
+    const T* __restrict__ y = static_cast<const T*>(a.y_perm);
     T* out = static_cast<T*>(a.out);
+    const int my_p = lane < k ? a.tok_pos[row * k + lane] : -1;
+    const float my_w = lane < k ? a.topk_w[row * k + lane] : 0.0f;
     // gated residual: the row's gate and input (block.rs:101)
     const float* grow = a.gate ? a.gate + row / a.seq * a.D : nullptr;
     const T* xrow = a.gate ? static_cast<const T*>(a.resid_x) + row * a.D : nullptr;
-    for (int c = lane; c < nchunk; c += kWave) {
-        float acc[EPC], xv[EPC];
-        if (grow) load16(xrow + (int64_t)c * EPC, xv);  // in flight with the y loads
+    for (int c0 = lane; c0 < nchunk; c0 += kWave * kBatch) {
+        float acc[kBatch][EPC], xv[kBatch][EPC];
 #pragma unroll
-        for (int i = 0; i < EPC; ++i) acc[i] = 0.0f;
+        for (int u = 0; u < kBatch; ++u) {
+            const int c = min(c0 + u * kWave, nchunk - 1);  // past the end: not stored
+            if (grow) load16(xrow + (int64_t)c * EPC, xv[u]);  // in flight with the y loads
+#pragma unroll
+            for (int i = 0; i < EPC; ++i) acc[u][i] = 0.0f;
+        }
         for (int j = 0; j < k; ++j) {
-            const int p = a.tok_pos[row * k + j];
-            const float w = a.topk_w[row * k + j];
+            const int p = j < kWave ? __builtin_amdgcn_readlane(my_p, j) : a.tok_pos[row * k + j];
+            const float w = j < kWave
+                                ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), j))
+                                : a.topk_w[row * k + j];
             if (p < 0 || p >= a.a_cap) continue;
-            float v[EPC];
-            load16(y + (int64_t)p * a.D + (int64_t)c * EPC, v);
+            float v[kBatch][EPC];
 #pragma unroll
-            for (int i = 0; i < EPC; ++i) acc[i] = acc[i] + v[i] * w;
-        }
-        if (grow) {  // out = x + y * gate, y and each step rounded to the model dtype
-            float g[EPC];
-            load_f32s<EPC>(grow + (int64_t)c * EPC, g);
+            for (int u = 0; u < kBatch; ++u)
+                load16(y + (int64_t)p * a.D + (int64_t)min(c0 + u * kWave, nchunk - 1) * EPC, v[u]);
 #pragma unroll
-            for (int i = 0; i < EPC; ++i)
-                acc[i] = seam_residual<T>(xv[i], Elt<T>::to_f32(Elt<T>::from_f32(acc[i])), g[i]);
+            for (int u = 0; u < kBatch; ++u)
+#pragma unroll
+                for (int i = 0; i < EPC; ++i) acc[u][i] = acc[u][i] + v[u][i] * w;
         }
-        store16(out + row * a.D + (int64_t)c * EPC, acc);
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int c = c0 + u * kWave;
+            if (c >= nchunk) continue;
+            if (grow) {  // out = x + y * gate, y and each step rounded to the model dtype
+                float g[EPC];
+                load_f32s<EPC>(grow + (int64_t)c * EPC, g);
+#pragma unroll
+                for (int i = 0; i < EPC; ++i)
+                    acc[u][i] = seam_residual<T>(xv[u][i], Elt<T>::to_f32(Elt<T>::from_f32(acc[u][i])),
+                                                 g[i]);
+            }
+            store16(out + row * a.D + (int64_t)c * EPC, acc[u]);
+        }
     }
 }
 
@@ -259,13 +352,15 @@ __global__ __launch_bounds__(256) void kblock_kernel(const T* __restrict__ x, T*
 template <typename T>
 hipError_t launch_dispatch_t(const DispatchArgs& a, hipStream_t s) {
     const int nblk = (int)((a.rows + kRouterRows - 1) / kRouterRows);
-    const size_t lds = sizeof(int) * 2 * 64 * a.k_slots;
-    if (lds > 65536) {
-        hipError_t err = hipFuncSetAttribute((const void*)dispatch_kernel<T>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (err != hipSuccess) return err;
-    }
-    hipLaunchKernelGGL(dispatch_kernel<T>, dim3(nblk), dim3(1024), lds, s, a);
+    if (nblk == 0) return hipSuccess;
+    if (a.nchunks != nblk || a.E_cols < 1 || a.E_cols > kMaxExperts + 1 || a.k_slots < 1 ||
+        a.k_slots > a.E_cols || a.BM < 1 || !dispatch_fits(a.E_cols, a.k_slots))
+        return hipErrorInvalidValue;
+    const size_t lds = dispatch_lds(a.E_cols, a.k_slots);
+    hipError_t err = hipFuncSetAttribute((const void*)dispatch_kernel<T>,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(dispatch_kernel<T>, dim3(nblk), dim3(kDispThreads), lds, s, a);
     return hipGetLastError();
 }
 
@@ -278,10 +373,7 @@ hipError_t launch_combine_t(const CombineArgs& a, hipStream_t s) {
 
 }  // namespace
 
-hipError_t launch_scan(const ScanArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(kScanThreads), 0, s, a);
-    return hipGetLastError();
-}
+bool dispatch_supported(int E_cols, int k_slots) { return dispatch_fits(E_cols, k_slots); }
 
 hipError_t launch_dispatch(DType dt, const DispatchArgs& a, hipStream_t s) {
     switch (dt) {

@@ -142,7 +142,6 @@ private:
     float* d_gap_ = nullptr;
     int32_t* d_pos_ = nullptr;
     int32_t* d_chunk_counts_ = nullptr;
-    int32_t* d_chunk_base_ = nullptr;
     int32_t* d_expert_count_ = nullptr;
     int32_t* d_expert_off_ = nullptr;
     TileInfo* d_tiles_ = nullptr;

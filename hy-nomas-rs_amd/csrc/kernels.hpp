@@ -2,8 +2,8 @@
 //
 // Pipeline of one forward (all on one stream):
 //   router  -> topk_idx / topk_w / gap per row, per-chunk expert histogram
-//   scan    -> per-chunk bases, expert counts/offsets, GEMM tile table
-//   dispatch-> stable permutation (tok_pos) + gather of x rows (x_perm)
+//   dispatch-> expert counts/offsets, GEMM tile table, stable permutation
+//              (tok_pos) + gather of x rows (x_perm)
 //   gemm_gate_up -> h = silu(x W_gate^T + b_gate) * (x W_up^T + b_up)
 //   gemm_down    -> y_perm = h W_down^T + b_down
 //   combine -> out[t] = sum over the row's slots (ascending expert) of w * y_perm
@@ -52,18 +52,6 @@ struct RouterArgs {
     int32_t* chunk_counts;  // nchunks x E_cols
 };
 
-struct ScanArgs {
-    const int32_t* chunk_counts;  // nchunks x E_cols
-    int nchunks;
-    int E_cols;
-    int BM;
-    int max_tiles;
-    int32_t* chunk_base;    // nchunks x E_cols
-    int32_t* expert_count;  // E_cols
-    int32_t* expert_off;    // E_cols + 1
-    TileInfo* tiles;        // max_tiles
-    int32_t* tile_total;    // 1
-};
 
 // K-blocked layout (MFMA path): a matrix of R rows and K columns is stored as
 // K / kKBlock column blocks, each R rows x kKBlock contiguous elements, i.e.
@@ -77,7 +65,14 @@ struct DispatchArgs {
     int64_t rows;
     int D, E_cols, k_slots;
     const int32_t* topk_idx;
-    const int32_t* chunk_base;
+    const int32_t* chunk_counts;  // nchunks x E_cols, from the router
+    int nchunks;
+    int BM;                 // GEMM tile rows
+    int max_tiles;
+    int32_t* expert_count;  // E_cols
+    int32_t* expert_off;    // E_cols + 1
+    TileInfo* tiles;        // max_tiles
+    int32_t* tile_total;    // 1
     int32_t* tok_pos;  // rows x k_slots
     void* x_perm;      // a_cap x D, row-major or K-blocked
     int64_t a_cap;     // rows of x_perm (positions must stay below)
@@ -121,12 +116,13 @@ struct CombineArgs {
 };
 
 size_t router_lds_bytes(int E);
+// Whether the dispatch kernel's LDS holds E_cols experts and k_slots slots per row.
+bool dispatch_supported(int E_cols, int k_slots);
 
 hipError_t launch_seam_h(DType dt, const SeamArgs& a, hipStream_t s);
 hipError_t launch_gated_residual(DType dt, const void* x, const void* y, const float* gate,
                                  void* out, int64_t rows, int D, int64_t seq, hipStream_t s);
 hipError_t launch_router(DType dt, const RouterArgs& a, hipStream_t s);
-hipError_t launch_scan(const ScanArgs& a, hipStream_t s);
 hipError_t launch_dispatch(DType dt, const DispatchArgs& a, hipStream_t s);
 // MFMA grouped GEMMs (bf16 / f16): W packed as described in moe_layer.cpp.
 hipError_t launch_gemm_gate_up_mfma(DType dt, const GemmArgs& a, hipStream_t s);

@@ -69,6 +69,14 @@ int MoeLayer::check_shape(const nomas_moe_config& cfg, int64_t dim, int64_t hidd
     if (cfg.experts > kMaxExperts)
         return set_error(NOMAS_ERR_INVALID_CONFIG, "experts=%lld exceeds the supported maximum %d",
                          (long long)cfg.experts, kMaxExperts);
+    {
+        const bool dense = cfg.shared_dense > 0.0;
+        const int ecols = (int)cfg.experts + (dense ? 1 : 0), kslots = (int)cfg.top_k + (dense ? 1 : 0);
+        if (!dispatch_supported(ecols, kslots))
+            return set_error(NOMAS_ERR_INVALID_CONFIG,
+                             "top_k=%lld with experts=%lld exceeds the dispatch kernel's LDS",
+                             (long long)cfg.top_k, (long long)cfg.experts);
+    }
     if (dtype < 0 || dtype > 2)
         return set_error(NOMAS_ERR_INVALID_CONFIG, "unknown dtype code %d", dtype);
     if (dim < 8 || dim % 8 != 0)
@@ -290,7 +298,6 @@ int MoeLayer::ensure_workspace(int64_t rows) {
     const size_t o_gap = take(sizeof(float) * cap);
     const size_t o_pos = take(sizeof(int32_t) * A);
     const size_t o_cc = take(sizeof(int32_t) * nch * Ecols_);
-    const size_t o_cb = take(sizeof(int32_t) * nch * Ecols_);
     const size_t o_ec = take(sizeof(int32_t) * Ecols_);
     const size_t o_eo = take(sizeof(int32_t) * (Ecols_ + 1));
     const size_t o_tiles = take(sizeof(TileInfo) * mt);
@@ -317,7 +324,6 @@ int MoeLayer::ensure_workspace(int64_t rows) {
     d_gap_ = reinterpret_cast<float*>(b + o_gap);
     d_pos_ = reinterpret_cast<int32_t*>(b + o_pos);
     d_chunk_counts_ = reinterpret_cast<int32_t*>(b + o_cc);
-    d_chunk_base_ = reinterpret_cast<int32_t*>(b + o_cb);
     d_expert_count_ = reinterpret_cast<int32_t*>(b + o_ec);
     d_expert_off_ = reinterpret_cast<int32_t*>(b + o_eo);
     d_tiles_ = reinterpret_cast<TileInfo*>(b + o_tiles);
@@ -425,18 +431,8 @@ int MoeLayer::forward_impl(const void* x, void* y, int64_t rows, hipStream_t s,
     STAGE(launch_router(dt_, ra, s), "router");
     if ((rc = mark(1))) return rc;
 
-    ScanArgs sa;
-    sa.chunk_counts = d_chunk_counts_;
-    sa.nchunks = nch;
-    sa.E_cols = (int)Ecols_;
-    sa.BM = BM_;
-    sa.max_tiles = mt;
-    sa.chunk_base = d_chunk_base_;
-    sa.expert_count = d_expert_count_;
-    sa.expert_off = d_expert_off_;
-    sa.tiles = d_tiles_;
-    sa.tile_total = d_tile_total_;
-    STAGE(launch_scan(sa, s), "scan");
+    // the scan of the chunk histograms is part of the dispatch kernel: the
+    // "scan" stage is empty
     if ((rc = mark(2))) return rc;
 
     DispatchArgs da;
@@ -446,7 +442,14 @@ int MoeLayer::forward_impl(const void* x, void* y, int64_t rows, hipStream_t s,
     da.E_cols = (int)Ecols_;
     da.k_slots = (int)kslots_;
     da.topk_idx = d_idx_;
-    da.chunk_base = d_chunk_base_;
+    da.chunk_counts = d_chunk_counts_;
+    da.nchunks = nch;
+    da.BM = BM_;
+    da.max_tiles = mt;
+    da.expert_count = d_expert_count_;
+    da.expert_off = d_expert_off_;
+    da.tiles = d_tiles_;
+    da.tile_total = d_tile_total_;
     da.tok_pos = d_pos_;
     da.x_perm = d_xperm_;
     da.a_cap = cap_rows_ * kslots_;

@@ -45,6 +45,7 @@ def test_config_validate_mirrors_reference():
 @pytest.mark.parametrize("cfg,dim,hidden,dtype,msg", [
     (nm.MoeConfig(4, 5), 64, 128, 0, "top_k"),
     (nm.MoeConfig(300, 2), 64, 128, 0, "maximum"),
+    (nm.MoeConfig(256, 200), 64, 128, 0, "dispatch"),  # slots of a 64-row chunk beyond its LDS
     (nm.MoeConfig(4, 2), 60, 128, 0, "multiple of 8"),
     (nm.MoeConfig(4, 2), 64, 0, 0, "hidden"),
     (nm.MoeConfig(4, 2), 64, 128, 7, "dtype"),
