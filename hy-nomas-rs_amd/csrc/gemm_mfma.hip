@@ -324,26 +324,29 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
 
     // Epilogue.  Lane (l16, lq) of block (i, j) holds token row
     // wm*WM + j*16 + l16 and weight rows wn*WN + i*16 + 4*lq + (0..3).
+    // Weight blocks outermost: each bias read from LDS serves all 8 token
+    // blocks (read per token block, every read's latency was paid 64 times).
     const float* bias = sBias - n0;  // indexed by output column
     T* out = static_cast<T*>(a.out);
+    if constexpr (MODE == kGateUp) {
+        // h is written K-blocked for the down GEMM: (row, c) at
+        // ((c / 32) * a_cap + row) * 32 + c % 32
 #pragma unroll
-    for (int j = 0; j < SM; ++j) {
-        const int m = wm * WM + j * 16 + l16;
-        if (m >= nrows) continue;
-        if (MODE == kGateUp) {
-            // h is written K-blocked for the down GEMM: (row, c) at
-            // ((c / 32) * a_cap + row) * 32 + c % 32
-            T* hrow = out + (int64_t)(row0 + m) * kKBlock;
+        for (int p = 0; p < SN / 4; ++p) {
 #pragma unroll
-            for (int p = 0; p < SN / 4; ++p) {
+            for (int b = 0; b < 2; ++b) {
+                // gate block 4p + b, its up block 4p + b + 2 (32-row interleave)
+                const int prow = n0 + wn * WN + p * 64 + b * 16 + 4 * lq;
+                const float4 bg = *reinterpret_cast<const float4*>(bias + prow);
+                const float4 bu = *reinterpret_cast<const float4*>(bias + prow + 32);
+                const float bgv[4] = {bg.x, bg.y, bg.z, bg.w};
+                const float buv[4] = {bu.x, bu.y, bu.z, bu.w};
+                const int hc = (n0 + wn * WN + p * 64) / 2 + b * 16 + 4 * lq;
+                T* hcol = out + (int64_t)(hc / kKBlock) * a.a_cap * kKBlock + hc % kKBlock;
 #pragma unroll
-                for (int b = 0; b < 2; ++b) {
-                    // gate block 4p + b, its up block 4p + b + 2 (32-row interleave)
-                    const int prow = n0 + wn * WN + p * 64 + b * 16 + 4 * lq;
-                    const float4 bg = *reinterpret_cast<const float4*>(bias + prow);
-                    const float4 bu = *reinterpret_cast<const float4*>(bias + prow + 32);
-                    const float bgv[4] = {bg.x, bg.y, bg.z, bg.w};
-                    const float buv[4] = {bu.x, bu.y, bu.z, bu.w};
+                for (int j = 0; j < SM; ++j) {
+                    const int m = wm * WM + j * 16 + l16;
+                    if (m >= nrows) continue;
                     T hv[4];
 #pragma unroll
                     for (int s = 0; s < 4; ++s) {
@@ -355,24 +358,26 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
                     }
                     uint2 raw;
                     __builtin_memcpy(&raw, hv, 8);
-                    const int hc = (n0 + wn * WN + p * 64) / 2 + b * 16 + 4 * lq;
-                    *reinterpret_cast<uint2*>(hrow + (int64_t)(hc / kKBlock) * a.a_cap * kKBlock +
-                                              hc % kKBlock) = raw;
+                    *reinterpret_cast<uint2*>(hcol + (int64_t)(row0 + m) * kKBlock) = raw;
                 }
             }
-        } else {
-            T* orow = out + (int64_t)(row0 + m) * N;
+        }
+    } else {
 #pragma unroll
-            for (int i = 0; i < SN; ++i) {
-                const int nb = n0 + wn * WN + i * 16 + 4 * lq;
-                const float4 b = *reinterpret_cast<const float4*>(bias + nb);
-                const float bv4[4] = {b.x, b.y, b.z, b.w};
+        for (int i = 0; i < SN; ++i) {
+            const int nb = n0 + wn * WN + i * 16 + 4 * lq;
+            const float4 b = *reinterpret_cast<const float4*>(bias + nb);
+            const float bv4[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int j = 0; j < SM; ++j) {
+                const int m = wm * WM + j * 16 + l16;
+                if (m >= nrows) continue;
                 T ov[4];
 #pragma unroll
                 for (int s = 0; s < 4; ++s) ov[s] = Elt<T>::from_f32(acc[i][j][s] + bv4[s]);
                 uint2 raw;
                 __builtin_memcpy(&raw, ov, 8);
-                *reinterpret_cast<uint2*>(orow + nb) = raw;
+                *reinterpret_cast<uint2*>(out + (int64_t)(row0 + m) * N + nb) = raw;
             }
         }
     }
