@@ -115,14 +115,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
     static_assert(MODE == kDown || SN % 4 == 0, "gate/up pairs are 2 blocks apart in groups of 4");
     static_assert(BK == kKBlock, "operands are K-blocked by the k step");
 
-    // One LDS object per stage (indices are compile-time after unrolling).
-    __shared__ __attribute__((aligned(16))) T sW0[BN * BK], sW1[BN * BK], sW2[BN * BK], sW3[BN * BK];
-    __shared__ __attribute__((aligned(16))) T sX0[BM * BK], sX1[BM * BK], sX2[BM * BK], sX3[BM * BK];
+    // The ring: S weight stages, then S token-row stages (offsets compile-time
+    // after unrolling).  The down GEMM's epilogue reuses it as one region.
+    __shared__ __attribute__((aligned(16))) T sRing[S * (BN + BM) * BK];
     // the tile's BN biases (f32), loaded by one direct-to-LDS instruction
     __shared__ __attribute__((aligned(16))) float sBias[BN];
     static_assert(BN * sizeof(float) == kWave * 16, "one 16-byte chunk per lane");
-    auto stW = [&](int s) -> T* { return s == 0 ? sW0 : s == 1 ? sW1 : s == 2 ? sW2 : sW3; };
-    auto stX = [&](int s) -> T* { return s == 0 ? sX0 : s == 1 ? sX1 : s == 2 ? sX2 : sX3; };
+    auto stW = [&](int s) -> T* { return sRing + s * BN * BK; };
+    auto stX = [&](int s) -> T* { return sRing + S * BN * BK + s * BM * BK; };
 
     const int N = a.N, K = a.K;
     const int KT_tile = K / BK;  // k steps of a whole tile
@@ -363,21 +363,52 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
             }
         }
     } else {
+        // y goes out through LDS, half of the tile's rows at a time: the
+        // waves of that half write their biased, rounded blocks (8 bytes per
+        // lane) into padded LDS rows, then all 256 threads store whole
+        // 512-byte row slices, 16 bytes each (64 scattered 8-byte stores per
+        // lane cost 24k cycles a tile, the staged form 19k).  The barriers are
+        // bare s_barriers after lgkmcnt(0): __syncthreads() would also wait
+        // for the global stores.
+        constexpr int kOS = BN * (int)sizeof(T) + 16;  // padded LDS row, bytes
+        static_assert(BM / 2 * kOS <= (int)sizeof(sRing), "half a tile fits the ring");
+        unsigned char* sO = reinterpret_cast<unsigned char*>(sRing);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();  // every wave is done with the ring
 #pragma unroll
-        for (int i = 0; i < SN; ++i) {
-            const int nb = n0 + wn * WN + i * 16 + 4 * lq;
-            const float4 b = *reinterpret_cast<const float4*>(bias + nb);
-            const float bv4[4] = {b.x, b.y, b.z, b.w};
+        for (int half = 0; half < 2; ++half) {
+            if (wm == half) {
 #pragma unroll
-            for (int j = 0; j < SM; ++j) {
-                const int m = wm * WM + j * 16 + l16;
-                if (m >= nrows) continue;
-                T ov[4];
+                for (int i = 0; i < SN; ++i) {
+                    const int nl = wn * WN + i * 16 + 4 * lq;
+                    const float4 b = *reinterpret_cast<const float4*>(bias + n0 + nl);
+                    const float bv4[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
-                for (int s = 0; s < 4; ++s) ov[s] = Elt<T>::from_f32(acc[i][j][s] + bv4[s]);
-                uint2 raw;
-                __builtin_memcpy(&raw, ov, 8);
-                *reinterpret_cast<uint2*>(out + (int64_t)(row0 + m) * N + nb) = raw;
+                    for (int j = 0; j < SM; ++j) {
+                        T ov[4];
+#pragma unroll
+                        for (int s = 0; s < 4; ++s) ov[s] = Elt<T>::from_f32(acc[i][j][s] + bv4[s]);
+                        uint2 raw;
+                        __builtin_memcpy(&raw, ov, 8);
+                        *reinterpret_cast<uint2*>(sO + (j * 16 + l16) * kOS + nl * (int)sizeof(T)) = raw;
+                    }
+                }
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            constexpr int kRowChunks = BN * (int)sizeof(T) / 16;
+            const int rows_h = min(BM / 2, nrows - half * (BM / 2));
+#pragma unroll 4
+            for (int q = tid; q < BM / 2 * kRowChunks; q += kThreads) {
+                const int rl = q / kRowChunks, ch = q % kRowChunks;
+                if (rl < rows_h)
+                    *reinterpret_cast<uint4*>(out + (int64_t)(row0 + half * (BM / 2) + rl) * N + n0 +
+                                              ch * (16 / (int)sizeof(T))) =
+                        *reinterpret_cast<const uint4*>(sO + rl * kOS + ch * 16);
+            }
+            if (half == 0) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                __builtin_amdgcn_s_barrier();  // the reads of the first half are done
             }
         }
     }
