@@ -117,6 +117,35 @@ def test_empty_and_overloaded_experts():
     assert (counts[4:] == 0).all() and counts.sum() == 900 * k
 
 
+@pytest.mark.parametrize("E", [8, 40, 96])
+def test_exact_ties_go_to_the_lowest_index(E):
+    # duplicated router rows give bit-identical logits; the reference's
+    # first-max-wins argmax (moe.rs:78-80) takes the lower expert.  Ties are
+    # exact here, so no row is exempt: indices must equal the oracle's on every
+    # row (E = 8 and 40 use the four-lanes-per-row selection, 96 the
+    # wave-parallel one; 40 and 96 span several 16-expert logit blocks).
+    D, H, k = 256, 128, 3
+    t, x = small_case(400, D, E, k, H, 29 + E, router_std=0.2)
+    wr = t[PATH + ".router.weight"]
+    wr[E - 1] = wr[1]        # across logit blocks for E > 16
+    wr[2] = wr[1]
+    wr[E // 2] = wr[0]
+    layer = layer_from_tensors(t, "bf16", D, H, E, k)
+    rt, rx = rounded(t, x, "bf16")
+    p, _ = nm.workloads.oracle_params(rt, E)
+    layer.forward(to_device(x, "bf16"))
+    torch.cuda.synchronize()
+    idx, _, counts, gap = layer.routing(400)
+    o_idx, _, o_logits, _ = O.route(rx, p["wr"], k)
+    assert np.array_equal(o_logits[:, 1], o_logits[:, 2]) and np.array_equal(o_logits[:, 1], o_logits[:, E - 1])
+    assert np.array_equal(idx, o_idx)
+    assert np.array_equal(counts, np.bincount(o_idx.ravel(), minlength=E))
+    # a selected duplicate implies its lower twins were selected first
+    sel = np.zeros((400, E), bool)
+    np.put_along_axis(sel, idx.astype(np.int64), True, axis=1)
+    assert not (sel[:, 2] & ~sel[:, 1]).any() and not (sel[:, E - 1] & ~sel[:, 1]).any()
+
+
 def test_k_equals_experts_mfma():
     run_case(200, 256, 4, 4, 256, "bf16", seed=23)
 
