@@ -239,6 +239,26 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < SN / 2; ++i) fa[i] = rdA(0, i);
     __builtin_amdgcn_sched_barrier(0);
+    // A tile of at most WM live token rows leaves the waves of the second
+    // token half (wm = 1) with padding rows only: they skip the MFMAs (their
+    // accumulators stay zero and the epilogue stores no padding row) but keep
+    // their share of the loads and every barrier, in the same order as the
+    // loop below.  At the chip's power limit the skipped MFMAs are time saved.
+    const bool pad_half = nrows <= WM && (uwave >> 1) == 1;
+    if (pad_half) {
+        for (int kt0 = 0; kt0 < KT; kt0 += S) {
+#pragma unroll
+            for (int u = 0; u < S; ++u) {
+                const int s = kt0 + u;
+#pragma unroll
+                for (int i = 0; i < SN / 2; ++i) dma(Q / 2 + i, cl(s + 2), (u + 2) % S);
+                wait_vmcnt<Q>();
+                __builtin_amdgcn_s_barrier();
+#pragma unroll
+                for (int i = SN / 2; i < SN; ++i) dma(i - SN / 2, cl(s + 3), (u + 3) % S);
+            }
+        }
+    } else
     for (int kt0 = 0; kt0 < KT; kt0 += S) {
 #pragma unroll
         for (int u = 0; u < S; ++u) {
