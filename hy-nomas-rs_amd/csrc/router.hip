@@ -8,17 +8,20 @@
 //    (~1e-8 on unit-scale logits).  f32 inputs: f64 matrix products
 //    (v_mfma_f64_16x16x4_f64, exact products, f64 sums).  Either way expert
 //    choice is decided far below the 1e-6 logit near-tie threshold.
-//  - Wave (g, q) computes rows 16g..16g+15 of the chunk against 16 experts at
-//    a time over the q-th quarter of D; the four quarters are added in a fixed
-//    order (q = 0, 1, 2, 3) through LDS, so results do not depend on timing.
+//  - Wave (g, q) computes rows 16g..16g+15 of the chunk against 16 NB experts
+//    per pass over x (NB = 1, 2, 4 blocks of 16 for up to 16, 32, more
+//    experts) over the q-th quarter of D; the four quarters are added into the
+//    logit slots in a fixed order (q = 0, 1, 2, 3), so results do not depend
+//    on timing.
 //    Each lane loads 16 contiguous bytes of its row (and of its expert's
 //    weights) per step and feeds them to consecutive MFMAs: the k index of
 //    MFMA i, lane group lg is k0 + lg * EPC + i, the same assignment for both
 //    operands, so the 4-deep MFMA k dimension reads whole 16-byte chunks.
-//  - Selection: with E <= 64 four lanes take a row (a quarter of its experts
-//    each, combined by two xor shuffles; waves 0-3, one per SIMD); with more
-//    experts it is wave-parallel over experts (max / sum / k rounds of argmax
-//    as xor-shuffle reductions across the wave).  Ties go to the
+//  - Selection: with E <= 16 four lanes take a row (waves 0-3, one per SIMD),
+//    with E <= 64 sixteen lanes (all waves), each lane a share of the row's
+//    experts, combined by xor shuffles; with more experts it is wave-parallel
+//    over experts (max / sum / k rounds of argmax as xor-shuffle reductions
+//    across the wave).  Ties go to the
 //    lowest expert index, the reference's first-max-wins argmax (moe.rs:78-80).
 //  - Gates: p = exp(l - max) / sum_E exp(l - max), w = p / (sum_selected p + 1e-9)
 //    (moe.rs:68,92-95), evaluated in f64 and stored as f32.
@@ -29,6 +32,8 @@
 //    gate `dense_coef` (moe.rs:103-106 adds it after the experts).
 //  The kernel reads x once (T*D*b bytes) and the router weights from L2.
 #include "kernels.hpp"
+
+#include <type_traits>
 
 namespace nomas {
 
@@ -84,20 +89,25 @@ __device__ __forceinline__ double wave_sum(double v) {
     return v;
 }
 
-// LDS layout (bytes): logits [64][E] f64, parts 1..3 of the current 16-expert
-// block [3][4 groups][16][16] f64, counts [E + 1] int.
+// LDS layout (bytes): logits [64][E] f64, counts [E + 1] int.
 __host__ __device__ inline size_t router_lds(int E) {
-    return sizeof(double) * ((size_t)kRouterRows * E + 3 * kGroups * 256) + sizeof(int) * (E + 1);
+    return sizeof(double) * (size_t)kRouterRows * E + sizeof(int) * (E + 1);
 }
 
-template <typename T>
+// Expert blocks of 16 per pass over x: every x chunk loaded feeds NB MFMAs.
+// The ring depth shrinks as NB grows so the loads in flight fit the
+// registers of 16 waves per CU.
+template <typename T, int NB> struct RouterPass {
+    static constexpr int kPre = NB == 1 ? 4 : (NB == 2 ? 3 : 2);
+};
+
+template <typename T, int NB>
 __global__ __launch_bounds__(kRouterThreads) void router_kernel(
     const T* __restrict__ x, const T* __restrict__ wr, int64_t rows, int D, int E, int k,
     int k_slots, float dense_coef, int32_t* __restrict__ topk_idx, float* __restrict__ topk_w,
     float* __restrict__ gap, int32_t* __restrict__ chunk_counts) {
     extern __shared__ double s_logit[];                                   // [kRouterRows][E]
-    double* s_part = s_logit + kRouterRows * E;                           // [3][kGroups][16][16]
-    int* s_cnt = reinterpret_cast<int*>(s_part + 3 * kGroups * 256);      // [E + 1]
+    int* s_cnt = reinterpret_cast<int*>(s_logit + (size_t)kRouterRows * E);  // [E + 1]
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int E_cols = E + (k_slots > k ? 1 : 0);
     for (int e = tid; e < E_cols; e += kRouterThreads) s_cnt[e] = 0;
@@ -117,117 +127,130 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
     // Loads run kPre steps ahead of the MFMAs (a ring of raw 16-byte chunks
     // in registers), so the memory latency of x is paid once per pipeline
     // fill, not once per step.
-    constexpr int kPre = 4;
+    constexpr int kPre = RouterPass<T, NB>::kPre;
     auto unpack = [](const uint4& raw, int i) -> double {
         Vec16<T> t;
         __builtin_memcpy(&t, &raw, 16);
         return (double)Elt<T>::to_f32(t.v[i]);
     };
-    for (int e0 = 0; e0 < E; e0 += 16) {
-        const int ex = e0 + r16;
-        const bool ex_ok = ex < E;
-        const T* wrr = wr + (int64_t)(ex_ok ? ex : 0) * D;
+    for (int e0 = 0; e0 < E; e0 += 16 * NB) {
         // Loads are unconditional from clamped addresses (a load whose address
         // or value is chosen by a condition becomes a flat load with a
         // scratch-resident zero); chunks past this part's steps or past D are
         // zeroed where they are used.  Rows past the end and experts past E
         // read row 0 / expert 0: their logits are never used.
-        auto fetch = [&](int st, uint4& xa, uint4& wa) {
+        const T* wrr[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int ex = e0 + 16 * b + r16;
+            wrr[b] = wr + (int64_t)(ex < E ? ex : 0) * D;
+        }
+        auto fetch = [&](int st, uint4& xa, uint4 (&wa)[NB]) {
             const int kk = min(max(min(st, s1 - 1), 0) * CK + lg * EPC, D - EPC);
             xa = *reinterpret_cast<const uint4*>(xr + kk);
-            wa = *reinterpret_cast<const uint4*>(wrr + kk);
+#pragma unroll
+            for (int b = 0; b < NB; ++b) wa[b] = *reinterpret_cast<const uint4*>(wrr[b] + kk);
         };
         auto live = [&](int st) { return st < s1 && st * CK + lg * EPC < D; };  // D % 8 == 0
-        uint4 xb[kPre], wb[kPre];
+        uint4 xb[kPre], wb[kPre][NB];
 #pragma unroll
         for (int p = 0; p < kPre; ++p) fetch(s0 + p, xb[p], wb[p]);
-        d4 c0 = {0.0, 0.0, 0.0, 0.0}, c1 = {0.0, 0.0, 0.0, 0.0};
+        d4 c0[NB], c1[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            c0[b] = d4{0.0, 0.0, 0.0, 0.0};
+            c1[b] = d4{0.0, 0.0, 0.0, 0.0};
+        }
         // whole turns of the ring: steps past s1 are zeroed, which adds exactly 0
         for (int st0 = s0; st0 < s1; st0 += kPre) {
 #pragma unroll
             for (int p = 0; p < kPre; ++p) {
                 if (!live(st0 + p)) {
                     xb[p] = make_uint4(0, 0, 0, 0);
-                    wb[p] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) wb[p][b] = make_uint4(0, 0, 0, 0);
                 }
-                if constexpr (sizeof(T) == 2) {
-                    // one 16x16x32 MFMA per step: the 32 products are exact in
-                    // f32 and summed there; each step's sums join the f64
-                    // accumulators in step order
-                    const f32x4_t m = Mfma16<T>::run(xb[p], wb[p]);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) c0[r] += (double)m[r];
-                } else {
+                for (int b = 0; b < NB; ++b) {
+                    if constexpr (sizeof(T) == 2) {
+                        // one 16x16x32 MFMA per step: the 32 products are exact
+                        // in f32 and summed there; each step's sums join the f64
+                        // accumulators in step order
+                        const f32x4_t m = Mfma16<T>::run(xb[p], wb[p][b]);
 #pragma unroll
-                    for (int i = 0; i < EPC; ++i) {
-                        const double xd = unpack(xb[p], i), wd = unpack(wb[p], i);
-                        if (i & 1) c1 = __builtin_amdgcn_mfma_f64_16x16x4f64(xd, wd, c1, 0, 0, 0);
-                        else c0 = __builtin_amdgcn_mfma_f64_16x16x4f64(xd, wd, c0, 0, 0, 0);
+                        for (int r = 0; r < 4; ++r) c0[b][r] += (double)m[r];
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < EPC; ++i) {
+                            const double xd = unpack(xb[p], i), wd = unpack(wb[p][b], i);
+                            if (i & 1) c1[b] = __builtin_amdgcn_mfma_f64_16x16x4f64(xd, wd, c1[b], 0, 0, 0);
+                            else c0[b] = __builtin_amdgcn_mfma_f64_16x16x4f64(xd, wd, c0[b], 0, 0, 0);
+                        }
                     }
                 }
                 fetch(st0 + p + kPre, xb[p], wb[p]);
             }
         }
-        const d4 c = c0 + c1;
         // lane holds expert column r16 of rows 4 lg + r (16-bit inputs) or
-        // lg + 4 r (f32) of the group; part 0 writes the logit slots, parts
-        // 1..3 their own buffers
-        __syncthreads();  // the previous block's reads of s_part are done
+        // lg + 4 r (f32) of the group.  logit = ((p0 + p1) + p2) + p3: the
+        // parts add into the logit slots one after another.
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int i = sizeof(T) == 2 ? 4 * lg + r : lg + 4 * r;
-            if (q == 0) {
-                if (ex_ok) s_logit[(g * 16 + i) * E + ex] = c[r];
-            } else {
-                s_part[((q - 1) * kGroups + g) * 256 + i * 16 + r16] = c[r];
-            }
-        }
-        __syncthreads();
-        // logit = ((p0 + p1) + p2) + p3
-        {
-            const int gg = tid >> 8, i = (tid >> 4) & 15, j = tid & 15;
-            if (e0 + j < E) {
-                double v = s_logit[(gg * 16 + i) * E + e0 + j];
+        for (int qq = 0; qq < kParts; ++qq) {
+            if (q == qq) {
 #pragma unroll
-                for (int p = 0; p < kParts - 1; ++p) v += s_part[(p * kGroups + gg) * 256 + i * 16 + j];
-                s_logit[(gg * 16 + i) * E + e0 + j] = v;
+                for (int b = 0; b < NB; ++b) {
+                    const int ex = e0 + 16 * b + r16;
+                    if (ex >= E) continue;
+                    const d4 c = sizeof(T) == 2 ? c0[b] : c0[b] + c1[b];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int i = sizeof(T) == 2 ? 4 * lg + r : lg + 4 * r;
+                        double* dst = &s_logit[(g * 16 + i) * E + ex];
+                        *dst = qq == 0 ? c[r] : *dst + c[r];
+                    }
+                }
             }
+            __syncthreads();
         }
     }
-    __syncthreads();
 
     if (E <= kWave) {
-        // Four lanes per row (waves 0-3, one per SIMD): lane sub of a row's
-        // quad takes experts sub, sub + 4, ...; max, sums and argmax combine
-        // over the quad with two xor shuffles.
-        if (wave < 4) {
-            const int lr = tid >> 2, sub = tid & 3;
+        // L lanes per row (4 for up to 16 experts: waves 0-3, one per SIMD;
+        // 16 above: all 16 waves): lane sub of a row's group takes experts
+        // sub, sub + L, ...; max, sums and argmax combine over the group with
+        // xor shuffles.
+        auto select_rows = [&](auto lanes) {
+            constexpr int L = decltype(lanes)::value;
+            if (wave >= L) return;
+            const int lr = tid / L, sub = tid % L;
             const int64_t orow = chunk_row0 + lr;
             const bool ok = orow < rows;  // lanes of missing rows still shuffle
             const double* lgt = s_logit + (ok ? lr : 0) * E;
-            auto quad_max = [](double v) {
-                v = fmax(v, __shfl_xor(v, 1));
-                return fmax(v, __shfl_xor(v, 2));
+            auto group_max = [](double v) {
+#pragma unroll
+                for (int o = 1; o < L; o <<= 1) v = fmax(v, __shfl_xor(v, o));
+                return v;
             };
-            auto quad_sum = [](double v) {
-                v += __shfl_xor(v, 1);
-                return v + __shfl_xor(v, 2);
+            auto group_sum = [](double v) {
+#pragma unroll
+                for (int o = 1; o < L; o <<= 1) v += __shfl_xor(v, o);
+                return v;
             };
             double m = -INFINITY;
-            for (int e = sub; e < E; e += 4) m = fmax(m, lgt[e]);
-            m = quad_max(m);
+            for (int e = sub; e < E; e += L) m = fmax(m, lgt[e]);
+            m = group_max(m);
             double s = 0.0;
-            for (int e = sub; e < E; e += 4) s += exp(lgt[e] - m);
-            s = quad_sum(s);
-            uint64_t sel = 0;  // all selected experts of the row (every lane of the quad)
+            for (int e = sub; e < E; e += L) s += exp(lgt[e] - m);
+            s = group_sum(s);
+            uint64_t sel = 0;  // all selected experts of the row (every lane of the group)
             double kth = INFINITY;
             for (int it = 0; it < k; ++it) {
                 double bv = 0.0;
                 int bi = -1;
-                for (int e = sub; e < E; e += 4)
+                for (int e = sub; e < E; e += L)
                     if (!((sel >> e) & 1ull) && (bi < 0 || lgt[e] > bv)) { bv = lgt[e]; bi = e; }
 #pragma unroll
-                for (int o = 1; o <= 2; o <<= 1) {  // first maximum wins: lowest index
+                for (int o = 1; o < L; o <<= 1) {  // first maximum wins: lowest index
                     const double ov = __shfl_xor(bv, o);
                     const int oi = __shfl_xor(bi, o);
                     if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
@@ -236,14 +259,14 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
                 kth = bv;
             }
             double best_un = -INFINITY, psel = 0.0;
-            for (int e = sub; e < E; e += 4) {
+            for (int e = sub; e < E; e += L) {
                 if ((sel >> e) & 1ull) psel += exp(lgt[e] - m) / s;
                 else best_un = fmax(best_un, lgt[e]);
             }
-            best_un = quad_max(best_un);
-            psel = quad_sum(psel);
+            best_un = group_max(best_un);
+            psel = group_sum(psel);
             if (ok) {
-                for (int e = sub; e < E; e += 4) {
+                for (int e = sub; e < E; e += L) {
                     if (!((sel >> e) & 1ull)) continue;
                     const int rank = __popcll(sel & ((1ull << e) - 1ull));  // ascending index
                     const double p = exp(lgt[e] - m) / s;
@@ -260,7 +283,9 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
                     }
                 }
             }
-        }
+        };
+        if (E <= 16) select_rows(std::integral_constant<int, 4>{});
+        else select_rows(std::integral_constant<int, 16>{});
         __syncthreads();
         for (int e = tid; e < E_cols; e += kRouterThreads)
             chunk_counts[(int64_t)blockIdx.x * E_cols + e] = s_cnt[e];
@@ -344,20 +369,32 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
         chunk_counts[(int64_t)blockIdx.x * E_cols + e] = s_cnt[e];
 }
 
+template <typename T, int NB>
+hipError_t launch_router_nb(const RouterArgs& a, hipStream_t s, int nblk) {
+    const size_t lds = router_lds(a.E);
+    if (lds > 65536) {
+        hipError_t err = hipFuncSetAttribute((const void*)router_kernel<T, NB>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (err != hipSuccess) return err;
+    }
+    hipLaunchKernelGGL((router_kernel<T, NB>), dim3(nblk), dim3(kRouterThreads), lds, s,
+                       (const T*)a.x, (const T*)a.wr, a.rows, a.D, a.E, a.k, a.k_slots,
+                       a.dense_coef, a.topk_idx, a.topk_w, a.gap, a.chunk_counts);
+    return hipGetLastError();
+}
+
 template <typename T>
 hipError_t launch_router_t(const RouterArgs& a, hipStream_t s) {
     const int nblk = (int)((a.rows + kRouterRows - 1) / kRouterRows);
     if (nblk == 0) return hipSuccess;
-    const size_t lds = router_lds(a.E);
-    if (lds > 65536) {
-        hipError_t err = hipFuncSetAttribute((const void*)router_kernel<T>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (err != hipSuccess) return err;
+    // f32 inputs (f64 MFMAs, two accumulators per block) take one block per pass
+    if constexpr (sizeof(T) == 4) {
+        return launch_router_nb<T, 1>(a, s, nblk);
+    } else {
+        if (a.E <= 16) return launch_router_nb<T, 1>(a, s, nblk);
+        if (a.E <= 32) return launch_router_nb<T, 2>(a, s, nblk);
+        return launch_router_nb<T, 4>(a, s, nblk);
     }
-    hipLaunchKernelGGL(router_kernel<T>, dim3(nblk), dim3(kRouterThreads), lds, s,
-                       (const T*)a.x, (const T*)a.wr, a.rows, a.D, a.E, a.k, a.k_slots,
-                       a.dense_coef, a.topk_idx, a.topk_w, a.gap, a.chunk_counts);
-    return hipGetLastError();
 }
 
 }  // namespace
