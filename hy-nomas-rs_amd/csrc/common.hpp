@@ -33,12 +33,16 @@ template <typename T> struct Vec16 {
 };
 
 template <typename T>
-__device__ __forceinline__ void load16(const T* p, float* out) {
-    const uint4 raw = *reinterpret_cast<const uint4*>(p);
+__device__ __forceinline__ void unpack16(const uint4& raw, float* out) {
     Vec16<T> t;
     __builtin_memcpy(&t, &raw, 16);
 #pragma unroll
     for (int i = 0; i < Vec16<T>::N; ++i) out[i] = Elt<T>::to_f32(t.v[i]);
+}
+
+template <typename T>
+__device__ __forceinline__ void load16(const T* p, float* out) {
+    unpack16<T>(*reinterpret_cast<const uint4*>(p), out);
 }
 
 template <typename T>

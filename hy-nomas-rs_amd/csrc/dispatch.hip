@@ -8,6 +8,7 @@
 // buffers, and combine sums a row's slots in ascending expert order, the order
 // of the reference's accumulation loop (moe.rs:98-102).
 #include <algorithm>
+#include <type_traits>
 
 #include "kernels.hpp"
 #include "seam.hpp"
@@ -259,7 +260,8 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
 // One wave per row: out[row] = sum_j w_j * y_perm[pos_j] over the row's slots
 // in ascending expert order (then the dense slot), accumulated in f32.  The
 // row's positions and gates are read once (lane j holds slot j) and broadcast
-// with readlane; each lane then has its chunks' k loads in flight together.
+// with readlane; each lane has up to 4 slots' loads of its chunks in flight
+// together.
 template <typename T>
 __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -285,21 +287,55 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
 #pragma unroll
             for (int i = 0; i < EPC; ++i) acc[u][i] = 0.0f;
         }
-        for (int j = 0; j < k; ++j) {
-            const int p = j < kWave ? __builtin_amdgcn_readlane(my_p, j) : a.tok_pos[row * k + j];
-            const float w = j < kWave
-                                ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), j))
-                                : a.topk_w[row * k + j];
-            if (p < 0 || p >= a.a_cap) continue;
-            float v[kBatch][EPC];
+        // N slots at a time: their N * kBatch loads are all in flight before
+        // the first is added; the adds keep ascending slot order
+        // (slots below 64 come from the lanes, later ones from memory)
+        auto slots = [&](auto n, auto from_lanes, int j0) {
+            constexpr int N = decltype(n)::value;
+            int p[N];
+            float w[N];
+            uint4 raw[N][kBatch];
 #pragma unroll
-            for (int u = 0; u < kBatch; ++u)
-                load16(y + (int64_t)p * a.D + (int64_t)min(c0 + u * kWave, nchunk - 1) * EPC, v[u]);
+            for (int t = 0; t < N; ++t) {
+                const int j = j0 + t;
+                if constexpr (decltype(from_lanes)::value) {
+                    p[t] = __builtin_amdgcn_readlane(my_p, j);
+                    w[t] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), j));
+                } else {
+                    p[t] = a.tok_pos[row * k + j];
+                    w[t] = a.topk_w[row * k + j];
+                }
+                // a slot without a position (none in a valid routing) adds 0 x row 0
+                const bool ok = p[t] >= 0 && p[t] < a.a_cap;
+                const int64_t pc = ok ? p[t] : 0;
+                w[t] = ok ? w[t] : 0.0f;
 #pragma unroll
-            for (int u = 0; u < kBatch; ++u)
+                for (int u = 0; u < kBatch; ++u)
+                    raw[t][u] = *reinterpret_cast<const uint4*>(
+                        y + pc * a.D + (int64_t)min(c0 + u * kWave, nchunk - 1) * EPC);
+            }
 #pragma unroll
-                for (int i = 0; i < EPC; ++i) acc[u][i] = acc[u][i] + v[u][i] * w;
+            for (int t = 0; t < N; ++t) {
+#pragma unroll
+                for (int u = 0; u < kBatch; ++u) {
+                    float v[EPC];
+                    unpack16<T>(raw[t][u], v);
+#pragma unroll
+                    for (int i = 0; i < EPC; ++i) acc[u][i] = acc[u][i] + v[i] * w[t];
+                }
+            }
+        };
+        using Lanes = std::true_type;
+        const int k1 = min(k, kWave);
+        int j0 = 0;
+        for (; j0 + 4 <= k1; j0 += 4) slots(std::integral_constant<int, 4>{}, Lanes{}, j0);
+        switch (k1 - j0) {
+            case 3: slots(std::integral_constant<int, 3>{}, Lanes{}, j0); break;
+            case 2: slots(std::integral_constant<int, 2>{}, Lanes{}, j0); break;
+            case 1: slots(std::integral_constant<int, 1>{}, Lanes{}, j0); break;
+            default: break;
         }
+        for (int j = kWave; j < k; ++j) slots(std::integral_constant<int, 1>{}, std::false_type{}, j);
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) {
             const int c = c0 + u * kWave;
