@@ -170,12 +170,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
     }
 
     f32x4_t acc[SN][SM];
-#pragma unroll
-    for (int i = 0; i < SN; ++i)
-#pragma unroll
-        for (int j = 0; j < SM; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.0f;
 
     // load q (0..Q-1) of step kt into ring slot `slot`: q < QW are weight
     // rows, the rest token rows
@@ -220,16 +214,30 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
     // slots that are never read again), which keeps the loop branch-free and
     // the wait counts constant.
     auto cl = [&](int kt) { return kt < KT ? kt : KT - 1; };
-    // Bias slice first: wave 0's oldest load, so the first wait (step 0
-    // landed) also covers it.  Read only by the epilogue.
-    if (uwave == 0)
-        lds_dma16(a.bias + (int64_t)e * N + n0, lane * 16, lds_addr(sBias));
+    // Bias slice first: wave 0's oldest load (zeros for the parts of a split
+    // tile after the first).  The accumulators start at it, set while the
+    // first steps' loads are in flight, so the epilogue adds no bias.
+    if (uwave == 0) {
+        if (wu.part == 0)
+            lds_dma16(a.bias + (int64_t)e * N + n0, lane * 16, lds_addr(sBias));
+        else
+            *reinterpret_cast<uint4*>(&sBias[lane * 4]) = make_uint4(0, 0, 0, 0);
+    }
 #pragma unroll
     for (int q = 0; q < Q; ++q) dma(q, 0, 0);
 #pragma unroll
     for (int q = 0; q < Q; ++q) dma(q, cl(1), 1);
 #pragma unroll
     for (int q = 0; q < Q / 2; ++q) dma(q, cl(2), 2);
+    wait_vmcnt<2 * Q + Q / 2>();   // wave 0: the bias has landed
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // ... and is visible to every wave
+#pragma unroll
+    for (int i = 0; i < SN; ++i) {
+        const float4 b = *reinterpret_cast<const float4*>(&sBias[wn * WN + i * 16 + 4 * lq]);
+#pragma unroll
+        for (int j = 0; j < SM; ++j) acc[i][j] = f32x4_t{b.x, b.y, b.z, b.w};
+    }
     wait_vmcnt<Q + Q / 2>();
     __builtin_amdgcn_s_barrier();  // bare: __syncthreads() would add a vmcnt(0) fence
     __builtin_amdgcn_sched_barrier(0);
@@ -241,7 +249,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     // A tile of at most WM live token rows leaves the waves of the second
     // token half (wm = 1) with padding rows only: they skip the MFMAs (their
-    // accumulators stay zero and the epilogue stores no padding row) but keep
+    // accumulators keep their start values and the epilogue stores no
+    // padding row) but keep
     // their share of the loads and every barrier, in the same order as the
     // loop below.  At the chip's power limit the skipped MFMAs are time saved.
     const bool pad_half = nrows <= WM && (uwave >> 1) == 1;
@@ -342,11 +351,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
         if (tid == 0) a.split_cnt[wu.slot] = 0;
     }
 
-    // Epilogue.  Lane (l16, lq) of block (i, j) holds token row
-    // wm*WM + j*16 + l16 and weight rows wn*WN + i*16 + 4*lq + (0..3).
-    // Weight blocks outermost: each bias read from LDS serves all 8 token
-    // blocks (read per token block, every read's latency was paid 64 times).
-    const float* bias = sBias - n0;  // indexed by output column
+    // Epilogue (the accumulators include the bias).  Lane (l16, lq) of block
+    // (i, j) holds token row wm*WM + j*16 + l16 and weight rows
+    // wn*WN + i*16 + 4*lq + (0..3).
     T* out = static_cast<T*>(a.out);
     if constexpr (MODE == kGateUp) {
         // h is written K-blocked for the down GEMM: (row, c) at
@@ -356,11 +363,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
                 // gate block 4p + b, its up block 4p + b + 2 (32-row interleave)
-                const int prow = n0 + wn * WN + p * 64 + b * 16 + 4 * lq;
-                const float4 bg = *reinterpret_cast<const float4*>(bias + prow);
-                const float4 bu = *reinterpret_cast<const float4*>(bias + prow + 32);
-                const float bgv[4] = {bg.x, bg.y, bg.z, bg.w};
-                const float buv[4] = {bu.x, bu.y, bu.z, bu.w};
                 const int hc = (n0 + wn * WN + p * 64) / 2 + b * 16 + 4 * lq;
                 T* hcol = out + (int64_t)(hc / kKBlock) * a.a_cap * kKBlock + hc % kKBlock;
 #pragma unroll
@@ -370,8 +372,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
                     T hv[4];
 #pragma unroll
                     for (int s = 0; s < 4; ++s) {
-                        const float g = acc[4 * p + b][j][s] + bgv[s];
-                        const float u = acc[4 * p + b + 2][j][s] + buv[s];
+                        const float g = acc[4 * p + b][j][s];
+                        const float u = acc[4 * p + b + 2][j][s];
                         // silu(g) * u; the reciprocal (1 ulp) is far inside the
                         // 16-bit rounding of h
                         hv[s] = Elt<T>::from_f32(g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u);
@@ -384,7 +386,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
         }
     } else {
         // y goes out through LDS, half of the tile's rows at a time: the
-        // waves of that half write their biased, rounded blocks (8 bytes per
+        // waves of that half write their rounded blocks (8 bytes per
         // lane) into padded LDS rows, then all 256 threads store whole
         // 512-byte row slices, 16 bytes each (64 scattered 8-byte stores per
         // lane cost 24k cycles a tile, the staged form 19k).  The barriers are
@@ -395,19 +397,20 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
         unsigned char* sO = reinterpret_cast<unsigned char*>(sRing);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();  // every wave is done with the ring
+        // lq again, from the lane counter (keeping the first one alive
+        // through the loop cost a spill)
+        const int lq_e = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) >> 4;
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
             if (wm == half) {
 #pragma unroll
                 for (int i = 0; i < SN; ++i) {
-                    const int nl = wn * WN + i * 16 + 4 * lq;
-                    const float4 b = *reinterpret_cast<const float4*>(bias + n0 + nl);
-                    const float bv4[4] = {b.x, b.y, b.z, b.w};
+                    const int nl = wn * WN + i * 16 + 4 * lq_e;
 #pragma unroll
                     for (int j = 0; j < SM; ++j) {
                         T ov[4];
 #pragma unroll
-                        for (int s = 0; s < 4; ++s) ov[s] = Elt<T>::from_f32(acc[i][j][s] + bv4[s]);
+                        for (int s = 0; s < 4; ++s) ov[s] = Elt<T>::from_f32(acc[i][j][s]);
                         uint2 raw;
                         __builtin_memcpy(&raw, ov, 8);
                         *reinterpret_cast<uint2*>(sO + (j * 16 + l16) * kOS + nl * (int)sizeof(T)) = raw;
