@@ -146,6 +146,20 @@ def test_exact_ties_go_to_the_lowest_index(E):
     assert not (sel[:, 2] & ~sel[:, 1]).any() and not (sel[:, E - 1] & ~sel[:, 1]).any()
 
 
+@pytest.mark.parametrize("E,k,dtype", [(16, 2, "bf16"), (24, 3, "bf16"), (32, 4, "f16"),
+                                       (48, 6, "bf16"), (64, 8, "f16"), (65, 8, "bf16")])
+def test_router_pass_widths(E, k, dtype):
+    # one pass over x covers 16, 32 or 64 experts (E <= 16, <= 32, more), with
+    # partly filled 16-expert blocks; the selection takes 4 lanes per row up to
+    # 16 experts, 16 lanes up to 64, the whole wave beyond
+    run_case(330, 256, E, k, 128, dtype, seed=40 + E, router_std=0.2)
+
+
+def test_more_than_64_slots_per_row():
+    # top-70 of 80: the combine reads slots past 64 from memory, not from lanes
+    run_case(100, 256, 80, 70, 128, "bf16", seed=39, router_std=0.2)
+
+
 def test_k_equals_experts_mfma():
     run_case(200, 256, 4, 4, 256, "bf16", seed=23)
 
