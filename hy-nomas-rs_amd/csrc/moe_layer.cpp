@@ -37,6 +37,13 @@ struct DeviceGuard {
 };
 
 inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// The end-of-forward event only orders a later forward on another stream of
+// the same device after this one: a device-scope release is enough (the
+// default system-scope release writes back and invalidates the caches and
+// idled the GPU for about 6 us per forward).  The stage-timing events take a
+// device-scope release for the same reason.
+constexpr unsigned kDoneFlags = hipEventDisableTiming | hipEventReleaseToDevice;
 }  // namespace
 
 int set_error(int code, const char* fmt, ...) {
@@ -501,7 +508,7 @@ int MoeLayer::forward_impl(const void* x, void* y, int64_t rows, hipStream_t s,
     STAGE(launch_combine(dt_, ca, s), "combine");
     if ((rc = mark(6))) return rc;
 #undef STAGE
-    if (!done_) HIP_TRY(hipEventCreateWithFlags(&done_, hipEventDisableTiming));
+    if (!done_) HIP_TRY(hipEventCreateWithFlags(&done_, kDoneFlags));
     HIP_TRY(hipEventRecord(done_, s));
     done_recorded_ = true;
     last_rows_ = rows;
@@ -570,7 +577,7 @@ int MoeLayer::forward_dense(const void* x, void* y, int64_t rows, hipStream_t s)
     if ((rc = mark(5))) return rc;
     if ((rc = mark(6))) return rc;
 #undef STAGE
-    if (!done_) HIP_TRY(hipEventCreateWithFlags(&done_, hipEventDisableTiming));
+    if (!done_) HIP_TRY(hipEventCreateWithFlags(&done_, kDoneFlags));
     HIP_TRY(hipEventRecord(done_, s));
     done_recorded_ = true;
     last_rows_ = rows;
@@ -635,7 +642,7 @@ int MoeLayer::set_profiling(bool on) {
     DeviceGuard g(device_);
     if (on && events_.empty()) {
         events_.resize((size_t)kRing * 7);
-        for (hipEvent_t& e : events_) HIP_TRY(hipEventCreate(&e));
+        for (hipEvent_t& e : events_) HIP_TRY(hipEventCreateWithFlags(&e, hipEventReleaseToDevice));
     }
     profiling_ = on;
     recorded_ = 0;
