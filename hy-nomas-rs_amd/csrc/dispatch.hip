@@ -180,7 +180,8 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
     __syncthreads();
     // 4. the copy
     constexpr int EPC = 16 / sizeof(T);
-    constexpr int kPPK = kKBlock * (int)sizeof(T) / 16;  // pieces of one row in one K-block
+    constexpr int KB = kblock_elems<T>();
+    constexpr int kPPK = kKBlockBytes / 16;  // pieces of one row in one K-block
     static_assert(kSlabPieces % kPPK == 0, "a slab holds whole K-blocks");
     const int nck = a.D / EPC;  // 16-byte chunks per row (D % 8 == 0)
     const int nslab = (nck + kSlabPieces - 1) / kSlabPieces;
@@ -248,7 +249,7 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
                 const uint4 val = *reinterpret_cast<const uint4*>(sb + s_prow[pr] * kSlabStride + h * 16);
                 const int64_t col = (int64_t)c * EPC;
                 const int64_t off = a.kblocked
-                    ? ((col / kKBlock) * a.a_cap + p) * kKBlock + col % kKBlock
+                    ? ((col / KB) * a.a_cap + p) * KB + col % KB
                     : (int64_t)p * a.D + col;
                 *reinterpret_cast<uint4*>(xp + off) = val;
             }
@@ -381,7 +382,8 @@ __global__ __launch_bounds__(256) void kblock_kernel(const T* __restrict__ x, T*
         const int64_t r = i / nchunk;
         const int64_t col = (i % nchunk) * EPC;
         const uint4 v = *reinterpret_cast<const uint4*>(x + r * D + col);
-        *reinterpret_cast<uint4*>(xk + ((col / kKBlock) * a_cap + r) * kKBlock + col % kKBlock) = v;
+        constexpr int KB = kblock_elems<T>();
+        *reinterpret_cast<uint4*>(xk + ((col / KB) * a_cap + r) * KB + col % KB) = v;
     }
 }
 
@@ -432,7 +434,8 @@ hipError_t launch_dense_tiles(int64_t rows, int BM, int max_tiles, TileInfo* til
 hipError_t launch_kblock(DType dt, const void* x, void* xk, int64_t rows, int D, int64_t a_cap,
                          hipStream_t s) {
     if (rows <= 0) return hipSuccess;
-    if (D % kKBlock != 0 || a_cap < rows) return hipErrorInvalidValue;
+    if ((int64_t)D * (int64_t)dtype_size(dt) % kKBlockBytes != 0 || a_cap < rows)
+        return hipErrorInvalidValue;
     const int64_t chunks = rows * (D / (16 / (int)dtype_size(dt)));
     const unsigned nblk = (unsigned)std::min<int64_t>((chunks + 255) / 256, 65536);
     switch (dt) {
@@ -443,6 +446,10 @@ hipError_t launch_kblock(DType dt, const void* x, void* xk, int64_t rows, int D,
         case DType::F16:
             hipLaunchKernelGGL(kblock_kernel<_Float16>, dim3(nblk), dim3(256), 0, s,
                                (const _Float16*)x, (_Float16*)xk, rows, D, a_cap);
+            break;
+        case DType::F32:
+            hipLaunchKernelGGL(kblock_kernel<float>, dim3(nblk), dim3(256), 0, s,
+                               (const float*)x, (float*)xk, rows, D, a_cap);
             break;
         default: return hipErrorInvalidValue;
     }

@@ -32,6 +32,8 @@
 //  - Block ids are mapped to tiles XCD-aware (tile_map.hpp): the XCDs work on
 //    one expert at a time (its weights shared through the MALL), each XCD on
 //    an 8 x 4 group of tiles that share panels in its own L2.
+#include <type_traits>
+
 #include "kernels.hpp"
 #include "tile_map.hpp"
 
@@ -43,24 +45,36 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
+// A lane's 16-byte operand fragment (one row, 64 bytes of k per stage split
+// over the 4 lane groups) feeds kSub MFMAs: one 16x16x32 for 16-bit types,
+// four 16x16x4 for f32 (MFMA t takes element t; lane group g then holds
+// k = 4 g + t of the stage, the same for both operands).
 template <typename T> struct Mfma;
 template <> struct Mfma<__bf16> {
     typedef bf16x8_t V;
-    static __device__ __forceinline__ f32x4_t run(V a, V b, f32x4_t c) {
+    static constexpr int kSub = 1;
+    static __device__ __forceinline__ f32x4_t run(V a, V b, f32x4_t c, int) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
     }
 };
 template <> struct Mfma<_Float16> {
     typedef f16x8_t V;
-    static __device__ __forceinline__ f32x4_t run(V a, V b, f32x4_t c) {
+    static constexpr int kSub = 1;
+    static __device__ __forceinline__ f32x4_t run(V a, V b, f32x4_t c, int) {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+};
+template <> struct Mfma<float> {
+    typedef f32x4_t V;
+    static constexpr int kSub = 4;
+    static __device__ __forceinline__ f32x4_t run(V a, V b, f32x4_t c, int t) {
+        return __builtin_amdgcn_mfma_f32_16x16x4f32(a[t], b[t], c, 0, 0, 0);
     }
 };
 
 enum { kGateUp = 0, kDown = 1 };
 
 constexpr int kThreads = 256;
-constexpr int kBK = 32;     // k step = one 16x16x32 MFMA
 constexpr int kStages = 4;  // LDS ring depth; the main loop is unrolled over one turn
 
 // Physical 16-byte chunk of logical chunk c in LDS row r is c ^ swz(r) (4
@@ -103,17 +117,19 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
     using V = typename Mfma<T>::V;
     constexpr int WM = BM / 2, WN = BN / 2;       // wave tile: token rows x weight rows
     constexpr int SM = WM / 16, SN = WN / 16;     // 16x16 MFMA blocks per wave
-    constexpr int CH = BK / 8;                    // 16-byte chunks per LDS row
+    constexpr int EPC = 16 / (int)sizeof(T);      // elements per 16-byte chunk
+    constexpr int CH = BK / EPC;                  // 16-byte chunks per LDS row
+    constexpr int kSub = Mfma<T>::kSub;
     constexpr int RPI = kWave / CH;               // rows filled by one load instruction
     constexpr int NW = kThreads / kWave;
     constexpr int QW = BN / RPI / NW;             // load instructions per wave per k step
     constexpr int QX = BM / RPI / NW;
     constexpr int Q = QW + QX;
-    static_assert(BK == 32 && CH == 4, "one 16x16x32 k step per stage");
+    static_assert(BK * (int)sizeof(T) == kKBlockBytes && CH == 4, "64 bytes of k per stage");
     static_assert(S == 4, "ring of 4 stages, the loop unrolled over one turn");
     static_assert(SN == 8 && SM == 8 && Q == 8, "row schedule: 8 x 8 blocks, 8 loads per step");
     static_assert(MODE == kDown || SN % 4 == 0, "gate/up pairs are 2 blocks apart in groups of 4");
-    static_assert(BK == kKBlock, "operands are K-blocked by the k step");
+    static_assert(BK == kblock_elems<T>(), "operands are K-blocked by the k step");
 
     // The ring: S weight stages, then S token-row stages (offsets compile-time
     // after unrolling).  The down GEMM's epilogue reuses it as one region.
@@ -160,13 +176,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < QW; ++i) {
         const int r = (wave * QW + i) * RPI + lane / CH;
-        woff[i] = (r * BK + (((lane % CH) ^ swz(r)) * 8)) * (int)sizeof(T);  // bytes
+        woff[i] = (r * BK + (((lane % CH) ^ swz(r)) * EPC)) * (int)sizeof(T);  // bytes
     }
 #pragma unroll
     for (int i = 0; i < QX; ++i) {
         const int r = (wave * QX + i) * RPI + lane / CH;
         const int rr = r < nrows ? r : nrows - 1;
-        xoff[i] = (rr * BK + (((lane % CH) ^ swz(r)) * 8)) * (int)sizeof(T);  // bytes
+        xoff[i] = (rr * BK + (((lane % CH) ^ swz(r)) * EPC)) * (int)sizeof(T);  // bytes
     }
 
     f32x4_t acc[SN][SM];
@@ -184,11 +200,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
     // operand fragments: lane (l16, lq) holds row l16 of a 16-row block, k chunk lq
     auto rdA = [&](int slot, int i) -> V {
         const int r = wn * WN + i * 16 + l16;
-        return *reinterpret_cast<const V*>(&stW(slot)[r * BK + ((lq ^ swz(r)) * 8)]);
+        return *reinterpret_cast<const V*>(&stW(slot)[r * BK + ((lq ^ swz(r)) * EPC)]);
     };
     auto rdB = [&](int slot, int j) -> V {
         const int r = wm * WM + j * 16 + l16;
-        return *reinterpret_cast<const V*>(&stX(slot)[r * BK + ((lq ^ swz(r)) * 8)]);
+        return *reinterpret_cast<const V*>(&stX(slot)[r * BK + ((lq ^ swz(r)) * EPC)]);
     };
 
     // Stage s (ring slot s % 4) runs the 64 MFMAs of k step s as 8 rows
@@ -283,10 +299,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
                 if (i < SN / 2) fa[SN / 2 + i] = rdA(u, SN / 2 + i);
                 else fa[i - SN / 2] = rdA((u + 1) % S, i - SN / 2);
 #pragma unroll
+                for (int t = 0; t < kSub; ++t)
+#pragma unroll
                 for (int j = 0; j < SM; ++j) {
-                    acc[i][j] = Mfma<T>::run(fa[i], fb[j], acc[i][j]);
-                    if (i == SN - 1) fb[j] = rdB((u + 1) % S, j);
-                    if (j == 1) {
+                    acc[i][j] = Mfma<T>::run(fa[i], fb[j], acc[i][j], t);
+                    if (t == kSub - 1 && i == SN - 1) fb[j] = rdB((u + 1) % S, j);
+                    if (t == 0 && j == 1) {
                         __builtin_amdgcn_sched_barrier(0);
                         if (i < SN / 2) dma(Q / 2 + i, cl(s + 2), (u + 2) % S);
                         else dma(i - SN / 2, cl(s + 3), (u + 3) % S);
@@ -355,16 +373,18 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
     // (i, j) holds token row wm*WM + j*16 + l16 and weight rows
     // wn*WN + i*16 + 4*lq + (0..3).
     T* out = static_cast<T*>(a.out);
+    // a lane's 4 consecutive output columns as one store
+    typedef typename std::conditional<sizeof(T) == 2, uint2, uint4>::type Raw4;
     if constexpr (MODE == kGateUp) {
         // h is written K-blocked for the down GEMM: (row, c) at
-        // ((c / 32) * a_cap + row) * 32 + c % 32
+        // ((c / BK) * a_cap + row) * BK + c % BK
 #pragma unroll
         for (int p = 0; p < SN / 4; ++p) {
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
                 // gate block 4p + b, its up block 4p + b + 2 (32-row interleave)
                 const int hc = (n0 + wn * WN + p * 64) / 2 + b * 16 + 4 * lq;
-                T* hcol = out + (int64_t)(hc / kKBlock) * a.a_cap * kKBlock + hc % kKBlock;
+                T* hcol = out + (int64_t)(hc / BK) * a.a_cap * BK + hc % BK;
 #pragma unroll
                 for (int j = 0; j < SM; ++j) {
                     const int m = wm * WM + j * 16 + l16;
@@ -374,26 +394,29 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
                     for (int s = 0; s < 4; ++s) {
                         const float g = acc[4 * p + b][j][s];
                         const float u = acc[4 * p + b + 2][j][s];
-                        // silu(g) * u; the reciprocal (1 ulp) is far inside the
-                        // 16-bit rounding of h
+                        // silu(g) * u; the reciprocal (1 ulp) and the exponential
+                        // add a few f32 ulps, far inside the output tolerance
                         hv[s] = Elt<T>::from_f32(g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u);
                     }
-                    uint2 raw;
-                    __builtin_memcpy(&raw, hv, 8);
-                    *reinterpret_cast<uint2*>(hcol + (int64_t)(row0 + m) * kKBlock) = raw;
+                    Raw4 raw;
+                    __builtin_memcpy(&raw, hv, sizeof(raw));
+                    *reinterpret_cast<Raw4*>(hcol + (int64_t)(row0 + m) * BK) = raw;
                 }
             }
         }
     } else {
-        // y goes out through LDS, half of the tile's rows at a time: the
-        // waves of that half write their rounded blocks (8 bytes per
-        // lane) into padded LDS rows, then all 256 threads store whole
-        // 512-byte row slices, 16 bytes each (64 scattered 8-byte stores per
-        // lane cost 24k cycles a tile, the staged form 19k).  The barriers are
-        // bare s_barriers after lgkmcnt(0): __syncthreads() would also wait
-        // for the global stores.
+        // y goes out through LDS, a part of the tile's rows at a time (halves
+        // for 16-bit types, quarters for f32): the waves owning those rows
+        // write their rounded blocks (4 values per lane) into padded LDS rows,
+        // then all 256 threads store whole row slices, 16 bytes each (64
+        // scattered 8-byte stores per lane cost 24k cycles a tile, the staged
+        // form 19k).  The barriers are bare s_barriers after lgkmcnt(0):
+        // __syncthreads() would also wait for the global stores.
+        constexpr int NP = sizeof(T) == 2 ? 2 : 4;     // row parts
+        constexpr int kPR = BM / NP;                   // rows per part
+        constexpr int kJP = SM * 2 / NP;               // a wave's token blocks per part
         constexpr int kOS = BN * (int)sizeof(T) + 16;  // padded LDS row, bytes
-        static_assert(BM / 2 * kOS <= (int)sizeof(sRing), "half a tile fits the ring");
+        static_assert(kPR * kOS <= (int)sizeof(sRing), "a part of the tile fits the ring");
         unsigned char* sO = reinterpret_cast<unsigned char*>(sRing);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();  // every wave is done with the ring
@@ -401,37 +424,38 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
         // through the loop cost a spill)
         const int lq_e = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) >> 4;
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            if (wm == half) {
+        for (int part = 0; part < NP; ++part) {
+            if (wm == part / (NP / 2)) {
+                const int j0 = (part % (NP / 2)) * kJP;
 #pragma unroll
                 for (int i = 0; i < SN; ++i) {
                     const int nl = wn * WN + i * 16 + 4 * lq_e;
 #pragma unroll
-                    for (int j = 0; j < SM; ++j) {
+                    for (int jj = 0; jj < kJP; ++jj) {
                         T ov[4];
 #pragma unroll
-                        for (int s = 0; s < 4; ++s) ov[s] = Elt<T>::from_f32(acc[i][j][s]);
-                        uint2 raw;
-                        __builtin_memcpy(&raw, ov, 8);
-                        *reinterpret_cast<uint2*>(sO + (j * 16 + l16) * kOS + nl * (int)sizeof(T)) = raw;
+                        for (int s = 0; s < 4; ++s) ov[s] = Elt<T>::from_f32(acc[i][j0 + jj][s]);
+                        Raw4 raw;
+                        __builtin_memcpy(&raw, ov, sizeof(raw));
+                        *reinterpret_cast<Raw4*>(sO + (jj * 16 + l16) * kOS + nl * (int)sizeof(T)) = raw;
                     }
                 }
             }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             __builtin_amdgcn_s_barrier();
             constexpr int kRowChunks = BN * (int)sizeof(T) / 16;
-            const int rows_h = min(BM / 2, nrows - half * (BM / 2));
+            const int rows_p = min(kPR, nrows - part * kPR);
 #pragma unroll 4
-            for (int q = tid; q < BM / 2 * kRowChunks; q += kThreads) {
+            for (int q = tid; q < kPR * kRowChunks; q += kThreads) {
                 const int rl = q / kRowChunks, ch = q % kRowChunks;
-                if (rl < rows_h)
-                    *reinterpret_cast<uint4*>(out + (int64_t)(row0 + half * (BM / 2) + rl) * N + n0 +
-                                              ch * (16 / (int)sizeof(T))) =
+                if (rl < rows_p)
+                    *reinterpret_cast<uint4*>(out + (int64_t)(row0 + part * kPR + rl) * N + n0 +
+                                              ch * EPC) =
                         *reinterpret_cast<const uint4*>(sO + rl * kOS + ch * 16);
             }
-            if (half == 0) {
+            if (part < NP - 1) {
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                __builtin_amdgcn_s_barrier();  // the reads of the first half are done
+                __builtin_amdgcn_s_barrier();  // the reads of this part are done
             }
         }
     }
@@ -441,14 +465,15 @@ template <typename T, int MODE>
 hipError_t launch_mfma_t(const GemmArgs& a, hipStream_t s) {
     constexpr int BM = kMfmaBM, BN = kMfmaBN;
     // whole column tiles, and whole turns of the ring in K
-    if (a.N % BN != 0 || a.K % (kBK * kStages) != 0) return hipErrorInvalidValue;
+    constexpr int BK = kblock_elems<T>();
+    if (a.N % BN != 0 || a.K % (BK * kStages) != 0) return hipErrorInvalidValue;
     if (a.split_ws == nullptr || a.split_cnt == nullptr) return hipErrorInvalidValue;
     // whole tiles, plus one round for the K-split units of a short last round
     static_assert(kSplitUnits == kRound, "the split units fill one round");
     const int64_t grid = tile_grid(a.max_tiles, a.N / BN) + kSplitUnits;
     if (a.max_tiles <= 0) return hipSuccess;
     if (grid > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((gemm_mfma_kernel<T, MODE, BM, BN, kBK, kStages>), dim3((unsigned)grid),
+    hipLaunchKernelGGL((gemm_mfma_kernel<T, MODE, BM, BN, BK, kStages>), dim3((unsigned)grid),
                        dim3(kThreads), 0, s, a);
     return hipGetLastError();
 }
@@ -458,12 +483,14 @@ hipError_t launch_mfma_t(const GemmArgs& a, hipStream_t s) {
 hipError_t launch_gemm_gate_up_mfma(DType dt, const GemmArgs& a, hipStream_t s) {
     if (dt == DType::BF16) return launch_mfma_t<__bf16, kGateUp>(a, s);
     if (dt == DType::F16) return launch_mfma_t<_Float16, kGateUp>(a, s);
+    if (dt == DType::F32) return launch_mfma_t<float, kGateUp>(a, s);
     return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemm_down_mfma(DType dt, const GemmArgs& a, hipStream_t s) {
     if (dt == DType::BF16) return launch_mfma_t<__bf16, kDown>(a, s);
     if (dt == DType::F16) return launch_mfma_t<_Float16, kDown>(a, s);
+    if (dt == DType::F32) return launch_mfma_t<float, kDown>(a, s);
     return hipErrorInvalidValue;
 }
 

@@ -54,11 +54,14 @@ struct RouterArgs {
 
 
 // K-blocked layout (MFMA path): a matrix of R rows and K columns is stored as
-// K / kKBlock column blocks, each R rows x kKBlock contiguous elements, i.e.
-// element (r, k) at ((k / kKBlock) * R + r) * kKBlock + k % kKBlock.  One
-// k step of a GEMM tile (256 rows x kKBlock) is then a single contiguous 16 KB
-// run of memory, fetched as whole 128-byte lines.
-constexpr int kKBlock = 32;
+// column blocks of KB = 64 bytes of elements (32 for 16-bit types, 16 for
+// f32), each R rows x KB contiguous elements, i.e. element (r, k) at
+// ((k / KB) * R + r) * KB + k % KB.  One k step of a GEMM tile (256 rows x
+// 64 bytes) is then a single contiguous 16 KB run of memory, fetched as whole
+// 128-byte lines.
+constexpr int kKBlockBytes = 64;
+template <typename T>
+__host__ __device__ constexpr int kblock_elems() { return kKBlockBytes / (int)sizeof(T); }
 
 struct DispatchArgs {
     const void* x;

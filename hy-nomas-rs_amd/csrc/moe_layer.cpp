@@ -102,7 +102,7 @@ MoeLayer::MoeLayer(const nomas_moe_config& cfg, int64_t dim, int64_t hidden, DTy
     const bool dense = cfg.shared_dense > 0.0;
     Ecols_ = E_ + (dense ? 1 : 0);
     kslots_ = k_ + (dense ? 1 : 0);
-    mfma_ = dt_ != DType::F32 && D_ % kMfmaBN == 0 && H_ % (kMfmaBN / 2) == 0;
+    mfma_ = D_ % kMfmaBN == 0 && H_ % (kMfmaBN / 2) == 0;
     BM_ = mfma_ ? kMfmaBM : kSimtBM;
 }
 
@@ -111,7 +111,7 @@ MoeLayer::MoeLayer(DenseTag, int64_t dim, int64_t hidden, DType dt, int device)
     Ecols_ = 1;
     kslots_ = 1;
     dense_only_ = true;
-    mfma_ = dt_ != DType::F32 && D_ % kMfmaBN == 0 && H_ % (kMfmaBN / 2) == 0;
+    mfma_ = D_ % kMfmaBN == 0 && H_ % (kMfmaBN / 2) == 0;
     BM_ = mfma_ ? kMfmaBM : kSimtBM;
 }
 
@@ -183,11 +183,11 @@ int MoeLayer::upload(const void* router_w, const void* gate_w, const void* gate_
                 src_row = p % H;
             }
             const uint8_t* src = (is_up ? uw : gw) + src_row * D * es;
-            if (mfma_) {  // K-blocked: (e, p, k) at ((e * D/32 + k/32) * 2H + p) * 32 + k % 32
-                const int64_t KB = D / kKBlock;
-                for (int64_t kb = 0; kb < KB; ++kb)
-                    std::memcpy(&w1[(size_t)(((e * KB + kb) * 2 * H + p) * kKBlock) * es],
-                                src + kb * kKBlock * es, (size_t)kKBlock * es);
+            if (mfma_) {  // K-blocked: (e, p, k) at ((e * D/KB + k/KB) * 2H + p) * KB + k % KB
+                const int64_t KB = kKBlockBytes / (int64_t)es, nkb = D / KB;
+                for (int64_t kb = 0; kb < nkb; ++kb)
+                    std::memcpy(&w1[(size_t)(((e * nkb + kb) * 2 * H + p) * KB) * es],
+                                src + kb * KB * es, (size_t)KB * es);
             } else {
                 std::memcpy(&w1[(size_t)((e * 2 * H + p) * D) * es], src, (size_t)D * es);
             }
@@ -200,12 +200,12 @@ int MoeLayer::upload(const void* router_w, const void* gate_w, const void* gate_
     std::vector<float> b2((size_t)(Ecols_ * D));
     for (int64_t e = 0; e < Ecols_; ++e) {
         const uint8_t* src = wsrc(down_w, dd_w, e, D * H);
-        if (mfma_) {  // K-blocked: (e, n, k) at ((e * H/32 + k/32) * D + n) * 32 + k % 32
-            const int64_t KB = H / kKBlock;
+        if (mfma_) {  // K-blocked: (e, n, k) at ((e * H/KB + k/KB) * D + n) * KB + k % KB
+            const int64_t KB = kKBlockBytes / (int64_t)es, nkb = H / KB;
             for (int64_t n = 0; n < D; ++n)
-                for (int64_t kb = 0; kb < KB; ++kb)
-                    std::memcpy(&w2[(size_t)(((e * KB + kb) * D + n) * kKBlock) * es],
-                                src + (n * H + kb * kKBlock) * es, (size_t)kKBlock * es);
+                for (int64_t kb = 0; kb < nkb; ++kb)
+                    std::memcpy(&w2[(size_t)(((e * nkb + kb) * D + n) * KB) * es],
+                                src + (n * H + kb * KB) * es, (size_t)KB * es);
         } else {
             std::memcpy(&w2[(size_t)(e * D * H) * es], src, (size_t)(D * H) * es);
         }

@@ -144,8 +144,8 @@ int nomas_moe_dims(const nomas_moe_t *h, int64_t *dim, int64_t *hidden, int64_t 
 int nomas_moe_set_profiling(nomas_moe_t *h, int enable);
 int nomas_moe_stage_times(nomas_moe_t *h, float *ms6);
 
-/* Which GEMM path the handle uses: 1 = bf16/f16 MFMA grouped GEMM,
- * 0 = general (any shape / f32) path. */
+/* Which GEMM path the handle uses: 1 = MFMA grouped GEMM (dim a multiple of
+ * 256 and hidden a multiple of 128, any dtype), 0 = general (any shape) path. */
 int nomas_moe_uses_mfma(const nomas_moe_t *h);
 
 void nomas_moe_destroy(nomas_moe_t *h);

@@ -57,7 +57,7 @@ def run(rows, dim, hidden, dtype, seed, bias=True):
     return ffn, x, got
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
 def test_mfma_path(dtype):
     ffn, _, _ = run(300, 256, 384, dtype, seed=41)
     assert ffn.uses_mfma
@@ -65,7 +65,7 @@ def test_mfma_path(dtype):
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_general_path(dtype):
-    # f32, and shapes the MFMA kernels do not tile, take the general path
+    # shapes the MFMA kernels do not tile take the general path
     ffn, _, _ = run(130, 72, 100, dtype, seed=42)
     assert not ffn.uses_mfma
 

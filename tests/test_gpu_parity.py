@@ -77,9 +77,16 @@ def test_general_path(dtype):
     assert not run_case(150, 72, 6, 2, 100, dtype, seed=11).uses_mfma
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
 def test_mfma_path(dtype):
     assert run_case(300, 256, 8, 2, 128, dtype, seed=12).uses_mfma
+
+
+def test_mfma_f32_ragged_split_tiles():
+    # f32 on the matrix cores (16x16x4 MFMAs): ragged expert tiles, several
+    # column tiles, a K long enough for the K-split tail, the quarter-tile
+    # staging of the down GEMM's output
+    run_case(900, 512, 4, 3, 384, "f32", seed=14)
 
 
 def test_mfma_multi_tile_ragged():
