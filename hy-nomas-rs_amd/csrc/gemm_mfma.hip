@@ -132,8 +132,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
     static_assert(BK == kblock_elems<T>(), "operands are K-blocked by the k step");
 
     // The ring: S weight stages, then S token-row stages (offsets compile-time
-    // after unrolling).  The down GEMM's epilogue reuses it as one region.
-    __shared__ __attribute__((aligned(16))) T sRing[S * (BN + BM) * BK];
+    // after unrolling).  The down GEMM's epilogue reuses it, extended to hold
+    // the rows of one staging round (all 256 for 16-bit types, 128 for f32).
+    constexpr int kRingBytes = S * (BN + BM) * BK * (int)sizeof(T);
+    constexpr int kRounds = sizeof(T) == 2 ? 1 : 2;          // down epilogue rounds
+    constexpr int kOS = BN * (int)sizeof(T) + 16;            // padded staging row, bytes
+    constexpr int kStageOut = MODE == kDown ? BM / kRounds * kOS : 0;
+    constexpr int kLdsBytes = kRingBytes > kStageOut ? kRingBytes : kStageOut;
+    __shared__ __attribute__((aligned(16))) unsigned char sMem[kLdsBytes];
+    T* const sRing = reinterpret_cast<T*>(sMem);
     // the tile's BN biases (f32), loaded by one direct-to-LDS instruction
     __shared__ __attribute__((aligned(16))) float sBias[BN];
     static_assert(BN * sizeof(float) == kWave * 16, "one 16-byte chunk per lane");
@@ -405,57 +412,50 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
             }
         }
     } else {
-        // y goes out through LDS, a part of the tile's rows at a time (halves
-        // for 16-bit types, quarters for f32): the waves owning those rows
-        // write their rounded blocks (4 values per lane) into padded LDS rows,
-        // then all 256 threads store whole row slices, 16 bytes each (64
-        // scattered 8-byte stores per lane cost 24k cycles a tile, the staged
-        // form 19k).  The barriers are bare s_barriers after lgkmcnt(0):
+        // y goes out through LDS in kRounds rounds (one for 16-bit types, two
+        // for f32): every wave writes its rounded blocks of the round (4 values
+        // per lane) into padded LDS rows, then all 256 threads store whole row
+        // slices, 16 bytes each (64 scattered 8-byte stores per lane cost 24k
+        // cycles a tile).  The barriers are bare s_barriers after lgkmcnt(0):
         // __syncthreads() would also wait for the global stores.
-        constexpr int NP = sizeof(T) == 2 ? 2 : 4;     // row parts
-        constexpr int kPR = BM / NP;                   // rows per part
-        constexpr int kJP = SM * 2 / NP;               // a wave's token blocks per part
-        constexpr int kOS = BN * (int)sizeof(T) + 16;  // padded LDS row, bytes
-        static_assert(kPR * kOS <= (int)sizeof(sRing), "a part of the tile fits the ring");
-        unsigned char* sO = reinterpret_cast<unsigned char*>(sRing);
+        constexpr int kJR = SM / kRounds;   // a wave's token blocks per round
+        constexpr int kWR = kJR * 16;       // a wave's rows per round
+        unsigned char* sO = sMem;
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();  // every wave is done with the ring
         // lq again, from the lane counter (keeping the first one alive
         // through the loop cost a spill)
         const int lq_e = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) >> 4;
 #pragma unroll
-        for (int part = 0; part < NP; ++part) {
-            if (wm == part / (NP / 2)) {
-                const int j0 = (part % (NP / 2)) * kJP;
+        for (int rd = 0; rd < kRounds; ++rd) {
 #pragma unroll
-                for (int i = 0; i < SN; ++i) {
-                    const int nl = wn * WN + i * 16 + 4 * lq_e;
+            for (int i = 0; i < SN; ++i) {
+                const int nl = wn * WN + i * 16 + 4 * lq_e;
 #pragma unroll
-                    for (int jj = 0; jj < kJP; ++jj) {
-                        T ov[4];
+                for (int jj = 0; jj < kJR; ++jj) {
+                    T ov[4];
 #pragma unroll
-                        for (int s = 0; s < 4; ++s) ov[s] = Elt<T>::from_f32(acc[i][j0 + jj][s]);
-                        Raw4 raw;
-                        __builtin_memcpy(&raw, ov, sizeof(raw));
-                        *reinterpret_cast<Raw4*>(sO + (jj * 16 + l16) * kOS + nl * (int)sizeof(T)) = raw;
-                    }
+                    for (int s = 0; s < 4; ++s) ov[s] = Elt<T>::from_f32(acc[i][rd * kJR + jj][s]);
+                    Raw4 raw;
+                    __builtin_memcpy(&raw, ov, sizeof(raw));
+                    *reinterpret_cast<Raw4*>(sO + (wm * kWR + jj * 16 + l16) * kOS + nl * (int)sizeof(T)) = raw;
                 }
             }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             __builtin_amdgcn_s_barrier();
+            // staging row sr = (wave half h, row w) holds tile row h * WM + rd * kWR + w
             constexpr int kRowChunks = BN * (int)sizeof(T) / 16;
-            const int rows_p = min(kPR, nrows - part * kPR);
 #pragma unroll 4
-            for (int q = tid; q < kPR * kRowChunks; q += kThreads) {
-                const int rl = q / kRowChunks, ch = q % kRowChunks;
-                if (rl < rows_p)
-                    *reinterpret_cast<uint4*>(out + (int64_t)(row0 + part * kPR + rl) * N + n0 +
-                                              ch * EPC) =
-                        *reinterpret_cast<const uint4*>(sO + rl * kOS + ch * 16);
+            for (int q = tid; q < 2 * kWR * kRowChunks; q += kThreads) {
+                const int sr = q / kRowChunks, ch = q % kRowChunks;
+                const int tr = (sr / kWR) * WM + rd * kWR + sr % kWR;
+                if (tr < nrows)
+                    *reinterpret_cast<uint4*>(out + (int64_t)(row0 + tr) * N + n0 + ch * EPC) =
+                        *reinterpret_cast<const uint4*>(sO + sr * kOS + ch * 16);
             }
-            if (part < NP - 1) {
+            if (rd < kRounds - 1) {
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                __builtin_amdgcn_s_barrier();  // the reads of this part are done
+                __builtin_amdgcn_s_barrier();  // the reads of this round are done
             }
         }
     }
