@@ -167,6 +167,19 @@ def test_more_than_64_slots_per_row():
     run_case(100, 256, 80, 70, 128, "bf16", seed=39, router_std=0.2)
 
 
+def test_routed_buffers_past_2_gib():
+    # 180,000 rows, top-2 of 8 at dim 3072: x_perm and y_perm hold 360,000
+    # routed rows (2.2 GB each), so their byte offsets pass 2^31.  Routing is
+    # checked on every row, the outputs on 96 rows spread over the range.
+    E, D, H, k, T = 8, 3072, 256, 2, 180_000
+    t, x = small_case(T, D, E, k, H, 31)
+    layer = layer_from_tensors(t, "bf16", D, H, E, k)
+    rt, rx = rounded(t, x, "bf16")
+    p, _ = nm.workloads.oracle_params(rt, E)
+    rows = np.linspace(0, T - 1, 96).astype(np.int64)
+    compare(layer, to_device(x, "bf16"), rx, p, k, "bf16", rows=rows)
+
+
 def test_k_equals_experts_mfma():
     run_case(200, 256, 4, 4, 256, "bf16", seed=23)
 
