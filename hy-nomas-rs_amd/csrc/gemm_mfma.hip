@@ -1,22 +1,25 @@
-// Grouped expert GEMMs on CDNA4 matrix cores (bf16 / f16 in, f32 accumulate).
+// Grouped expert GEMMs on CDNA4 matrix cores (bf16 / f16 / f32 in, f32
+// accumulate).
 //
 // Problem per expert e (rows of x_perm / h that belong to e):
 //   gate/up:  h[m, :] = silu(x W_gate^T + b_gate) * (x W_up^T + b_up)   K = D, N = 2H
 //   down:     y[m, :] = h W_down^T + b_down                              K = H, N = D
 // (hy-nomas-rs mlp.rs:42-46 applied to the rows routed to e).
 //
-// Work unit: a 256 x 256 output tile of one expert.  The scan kernel lists
-// the experts' 256-row tiles; the grid enumerates (row tile, column tile).
+// Work unit: a 256 x 256 output tile of one expert.  The dispatch kernel
+// lists the experts' 256-row tiles; the grid enumerates (row tile, column
+// tile).
 //  - Operands: weights are the MFMA "A" operand (rows = output columns),
 //    token rows the "B" operand, so each lane's accumulator holds 4
-//    consecutive output columns of one token row (8-byte stores).
-//  - v_mfma_f32_16x16x32_{bf16,f16}: 4 waves in a 2 x 2 grid, each wave a
+//    consecutive output columns of one token row.
+//  - v_mfma_f32_16x16x32_{bf16,f16} (f32: four v_mfma_f32_16x16x4f32 per
+//    16-byte fragment): 4 waves in a 2 x 2 grid, each wave a
 //    128 x 128 tile of 8 x 8 MFMA blocks (256 f32 accumulators per lane, in
 //    AGPRs).  The 16x16x32 form does the same work per cycle as 32x32x16 for
 //    less power, which matters because these GEMMs run at the power limit.
-//  - K is walked 32 at a time (one MFMA k step) through a ring of 4 LDS
-//    stages filled by direct global->LDS loads (global_load_lds_dwordx4, no
-//    VGPR staging), issued 2-3 steps ahead.  Operands are K-blocked in memory
+//  - K is walked 64 bytes at a time (32 elements, 16 for f32) through a ring
+//    of 4 LDS stages filled by direct global->LDS loads
+//    (global_load_lds_dwordx4, no VGPR staging), issued 2-3 steps ahead.  Operands are K-blocked in memory
 //    (kernels.hpp): one k step of a tile is a single contiguous 16 KB run.
 //  - LDS rows (64 bytes) keep their 16-byte chunks XOR-swizzled by row bits
 //    1-2, so the 16-row operand reads (ds_read_b128) are free of bank
