@@ -30,7 +30,13 @@ def rel_err(got, ref) -> float:
 
 
 def check_routing(layer, rows, o_idx, o_w, o_gap, E):
-    """Indices bit-exact and counts exact except on near ties; gates to f32 precision."""
+    """Indices bit-exact and counts exact except on near ties; gates to 1e-5 relative.
+
+    The 16-bit router sums each 32-term block of exact products in f32 before
+    the f64 accumulation, so a logit carries about 1e-7 of its own scale in
+    rounding; gates follow logit differences, and with logits of scale ~16
+    (router std 0.5 at dim 1024) that reaches a few 1e-6.
+    """
     idx, w, counts, gap = layer.routing(rows)
     near = o_gap < NEAR_TIE
     assert np.array_equal(idx[~near], o_idx[~near]), (
@@ -40,7 +46,7 @@ def check_routing(layer, rows, o_idx, o_w, o_gap, E):
         assert np.abs(counts - want_counts).sum() <= 2 * int(near.sum()) * o_idx.shape[1]
     else:
         assert np.array_equal(counts, want_counts)
-    np.testing.assert_allclose(w[~near], o_w[~near], rtol=2e-6, atol=1e-7)
+    np.testing.assert_allclose(w[~near], o_w[~near], rtol=1e-5, atol=1e-7)
     return near
 
 
