@@ -9,11 +9,14 @@ construction (the dispatch kernel's LDS limit) are skipped.
 """
 import random
 
+import numpy as np
 import pytest
+import torch
 
 import nomas_moe as nm
+import oracle as O
 from _common import rounded, small_case
-from _gpu import compare, layer_from_tensors, to_device
+from _gpu import TOL, check_routing, compare, layer_from_tensors, rel_err, to_device
 
 pytestmark = pytest.mark.gpu
 
@@ -48,3 +51,57 @@ def test_random_configuration(rows, D, E, k, H, dt, s, std, seed):
     rt, rx = rounded(t, x, dt)
     p, dn = nm.workloads.oracle_params(rt, E)
     compare(layer, to_device(x, dt), rx, p, k, dt, shared_dense=s, dense=dn)
+
+
+def _block_cases(seed=20261203, n=12):
+    rng = random.Random(seed)
+    out = []
+    for c in range(n):
+        B = rng.choice([1, 2, 3])
+        S = rng.choice([1, 17, 64, 300])
+        D = rng.choice([64, 256, 264, 512])
+        H = rng.choice([96, 128, 256])
+        E = rng.choice([1, 4, 8, 17, 40])
+        k = rng.randint(1, min(E, 4))
+        s = rng.choice([0.0, 0.5])
+        dt = rng.choice(["bf16", "f16", "f32"])
+        affine = rng.choice([True, False])
+        out.append((B, S, D, E, k, H, dt, s, affine, 4000 + c))
+    return out
+
+
+@pytest.mark.parametrize("B,S,D,E,k,H,dt,s,affine,seed", _block_cases())
+def test_random_block_configuration(B, S, D, E, k, H, dt, s, affine, seed):
+    """forward_block (norm2 + modulate, MoE, gated residual) on seeded random shapes."""
+    from test_gpu_block import block_case, dev
+    print(f"block sweep B={B} S={S} D={D} E={E} k={k} H={H} {dt} dense={s} affine={affine} "
+          f"seed={seed}", flush=True)
+    try:
+        layer, x, xm, sh, sc, g, nw, p, dn = block_case(B, S, D, E, k, H, dt, seed, s, affine)
+    except nm.NomasError as e:
+        pytest.skip(f"rejected by the library: {e}")
+    out = layer.forward_block(to_device(x, dt).reshape(B, S, D), dev(sh), dev(sc), dev(g), dev(nw))
+    torch.cuda.synchronize()
+    h1, _ = O.norm_modulate(xm, sh, sc, S, nw, 1e-6, dt, pow_mode=1)
+    o_idx, o_w, _, o_gap = O.route(h1, p["wr"], k)
+    near = check_routing(layer, B * S, o_idx, o_w, o_gap, E)
+    ref, _, _, _ = O.block_ffn(xm, p, k, sh, sc, g, S, nw, 1e-6, dt, pow_mode=0,
+                               shared_dense=s, dense=dn)
+    got = out.reshape(B * S, D).float().cpu().numpy()
+    err = rel_err(got[~near], ref[~near])
+    print(f"  rel err {err:.3e}, near ties {int(near.sum())}, mfma={layer.uses_mfma}", flush=True)
+    assert np.isfinite(got).all() and err <= TOL[dt]
+
+
+def _ffn_cases(seed=20261204, n=8):
+    rng = random.Random(seed)
+    return [(rng.choice([1, 33, 256, 700, 2000]), rng.choice([64, 72, 256, 512]),
+             rng.choice([96, 128, 256, 384]), rng.choice(["bf16", "f16", "f32"]),
+             rng.choice([True, False]), 5000 + c) for c in range(n)]
+
+
+@pytest.mark.parametrize("rows,D,H,dt,bias,seed", _ffn_cases())
+def test_random_ffn_configuration(rows, D, H, dt, bias, seed):
+    """The dense SwiGLU FFN (mlp.rs:42-46) on seeded random shapes."""
+    from test_gpu_ffn import run
+    run(rows, D, H, dt, seed, bias=bias)
