@@ -152,7 +152,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
 
     const int N = a.N, K = a.K;
     const int KT_tile = K / BK;  // k steps of a whole tile
-    // live row tiles (the scan never lists more than max_tiles)
+    // live row tiles (the dispatch never lists more than max_tiles)
     const int live = min(*a.tile_total, a.max_tiles);
     WorkUnit wu;
     if (!unit_coords(blockIdx.x, N / BN, live, KT_tile / S, &wu)) return;
