@@ -3,9 +3,13 @@
 // error convention.
 #pragma once
 
+#include <condition_variable>
 #include <cstdint>
 #include <map>
+#include <memory>
+#include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/nomas_moe.h"
@@ -18,6 +22,44 @@ namespace nomas {
 int set_error(int code, const char* fmt, ...);
 const char* last_error();
 void clear_error();
+
+// ---- host <-> device copies for the host-tensor forward (host_copy.cpp) ----
+// memcpy split over a few persistent worker threads (the caller takes a part)
+class CopyPool {
+public:
+    explicit CopyPool(int workers);
+    ~CopyPool();
+    void copy(void* dst, const void* src, size_t n);
+
+private:
+    void loop(int part);
+    void range(int part, size_t* b, size_t* e) const;
+    std::vector<std::thread> threads_;
+    std::mutex m_;
+    std::condition_variable cv_work_, cv_done_;
+    uint64_t gen_ = 0;
+    int remaining_ = 0;
+    bool stop_ = false;
+    const int parts_;
+    unsigned char* dst_ = nullptr;
+    const unsigned char* src_ = nullptr;
+    size_t n_ = 0;
+};
+
+// Pageable host memory <-> device through two pinned staging buffers, the
+// host copies of one chunk overlapping the DMA of the other.
+class HostStager {
+public:
+    ~HostStager();
+    int to_device(void* dst_dev, const void* src_host, size_t bytes, hipStream_t s);
+    int to_host(void* dst_host, const void* src_dev, size_t bytes, hipStream_t s);
+
+private:
+    int ensure();
+    void* pin_[2] = {nullptr, nullptr};
+    hipEvent_t ev_[2] = {nullptr, nullptr};
+    std::unique_ptr<CopyPool> pool_;
+};
 
 // ---- generator (generator.cpp) -------------------------------------------
 uint64_t path_seed(uint64_t seed, const char* path);
@@ -137,6 +179,11 @@ private:
     // workspace (sized for cap_rows_)
     int64_t cap_rows_ = 0;
     void* d_ws_ = nullptr;
+    // forward_host: device copies of x and y, kept between calls (grown as
+    // needed), and the pinned staging of the copies
+    void* d_hio_ = nullptr;
+    size_t hio_bytes_ = 0;  // bytes of each of the two halves
+    HostStager stager_;
     int32_t* d_idx_ = nullptr;
     float* d_w_ = nullptr;
     float* d_gap_ = nullptr;

@@ -1,0 +1,180 @@
+// Copies between pageable host memory and the device for the host-tensor
+// forward: through two pinned staging buffers of kChunk bytes, in chunks, so
+// that the host-side memcpy of one chunk (spread over a small pool of worker
+// threads) overlaps the DMA of the previous one.  hipMemcpy from pageable
+// memory stages through the runtime's own buffers with one host thread and
+// reached about 19 GB/s here; pinned-to-device DMA runs at about 55 GB/s.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <thread>
+
+#include "host.hpp"
+
+namespace nomas {
+
+namespace {
+constexpr size_t kChunk = (size_t)16 << 20;  // bytes per staging buffer
+constexpr size_t kMinSplit = (size_t)1 << 20;  // smaller copies stay on the calling thread
+}  // namespace
+
+CopyPool::CopyPool(int workers) : parts_(workers + 1) {
+    for (int i = 0; i < workers; ++i) threads_.emplace_back([this, i] { loop(i + 1); });
+}
+
+CopyPool::~CopyPool() {
+    {
+        std::lock_guard<std::mutex> l(m_);
+        stop_ = true;
+    }
+    cv_work_.notify_all();
+    for (std::thread& t : threads_) t.join();
+}
+
+// Part p of the current copy: 64-byte aligned slices, the last one takes the rest.
+void CopyPool::range(int p, size_t* b, size_t* e) const {
+    const size_t per = (n_ / parts_ + 63) & ~(size_t)63;
+    *b = std::min(n_, (size_t)p * per);
+    *e = p == parts_ - 1 ? n_ : std::min(n_, *b + per);
+}
+
+void CopyPool::loop(int p) {
+    uint64_t seen = 0;
+    for (;;) {
+        {
+            std::unique_lock<std::mutex> l(m_);
+            cv_work_.wait(l, [&] { return stop_ || gen_ != seen; });
+            if (stop_) return;
+            seen = gen_;
+        }
+        size_t b, e;
+        range(p, &b, &e);
+        if (e > b) std::memcpy(dst_ + b, src_ + b, e - b);
+        std::lock_guard<std::mutex> l(m_);
+        if (--remaining_ == 0) cv_done_.notify_one();
+    }
+}
+
+void CopyPool::copy(void* dst, const void* src, size_t n) {
+    if (n < kMinSplit || parts_ == 1) {
+        std::memcpy(dst, src, n);
+        return;
+    }
+    {
+        std::lock_guard<std::mutex> l(m_);
+        dst_ = static_cast<unsigned char*>(dst);
+        src_ = static_cast<const unsigned char*>(src);
+        n_ = n;
+        remaining_ = parts_ - 1;
+        ++gen_;
+    }
+    cv_work_.notify_all();
+    size_t b, e;
+    range(0, &b, &e);
+    if (e > b) std::memcpy(dst_ + b, src_ + b, e - b);
+    std::unique_lock<std::mutex> l(m_);
+    cv_done_.wait(l, [&] { return remaining_ == 0; });
+}
+
+// Host memory that is already pinned (hipHostMalloc'd, or a framework's pinned
+// tensor) goes straight to the DMA engine.  hipPointerGetAttributes fails on
+// pageable memory; that error is cleared so that a later launch check does
+// not report it.
+bool is_pinned(const void* p) {
+    hipPointerAttribute_t at;
+    const hipError_t e = hipPointerGetAttributes(&at, p);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return at.type == hipMemoryTypeHost;
+}
+
+HostStager::~HostStager() {
+    for (int b = 0; b < 2; ++b) {
+        if (ev_[b]) (void)hipEventDestroy(ev_[b]);
+        if (pin_[b]) (void)hipHostFree(pin_[b]);
+    }
+}
+
+int HostStager::ensure() {
+    if (pin_[0]) return NOMAS_OK;
+    for (int b = 0; b < 2; ++b) {
+        hipError_t e = hipHostMalloc(&pin_[b], kChunk, hipHostMallocDefault);
+        if (e != hipSuccess)
+            return set_error(NOMAS_ERR_OUT_OF_MEMORY, "hipHostMalloc of a staging buffer failed: %s",
+                             hipGetErrorString(e));
+        e = hipEventCreateWithFlags(&ev_[b], hipEventDisableTiming);
+        if (e != hipSuccess)
+            return set_error(NOMAS_ERR_HIP, "hipEventCreate failed: %s", hipGetErrorString(e));
+    }
+    const unsigned hw = std::thread::hardware_concurrency();
+    pool_.reset(new CopyPool((int)std::min(7u, hw > 2 ? hw / 2 - 1 : 0u)));
+    return NOMAS_OK;
+}
+
+#define STAGE_TRY(expr, what)                                                                  \
+    do {                                                                                       \
+        hipError_t _e = (expr);                                                                \
+        if (_e != hipSuccess) return set_error(NOMAS_ERR_HIP, "%s failed: %s", what, hipGetErrorString(_e)); \
+    } while (0)
+
+int HostStager::to_device(void* dst, const void* src, size_t bytes, hipStream_t s) {
+    if (is_pinned(src)) {
+        STAGE_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s), "hipMemcpyAsync H2D");
+        return NOMAS_OK;
+    }
+    int rc = ensure();
+    if (rc != NOMAS_OK) return rc;
+    const unsigned char* in = static_cast<const unsigned char*>(src);
+    unsigned char* out = static_cast<unsigned char*>(dst);
+    int c = 0;
+    for (size_t off = 0; off < bytes; off += kChunk, ++c) {
+        const size_t n = std::min(kChunk, bytes - off);
+        const int b = c & 1;
+        if (c >= 2) STAGE_TRY(hipEventSynchronize(ev_[b]), "hipEventSynchronize");  // buffer b drained
+        pool_->copy(pin_[b], in + off, n);
+        STAGE_TRY(hipMemcpyAsync(out + off, pin_[b], n, hipMemcpyHostToDevice, s), "hipMemcpyAsync H2D");
+        STAGE_TRY(hipEventRecord(ev_[b], s), "hipEventRecord");
+    }
+    return NOMAS_OK;
+}
+
+int HostStager::to_host(void* dst, const void* src, size_t bytes, hipStream_t s) {
+    if (is_pinned(dst)) {
+        STAGE_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s), "hipMemcpyAsync D2H");
+        STAGE_TRY(hipStreamSynchronize(s), "hipStreamSynchronize");
+        return NOMAS_OK;
+    }
+    int rc = ensure();
+    if (rc != NOMAS_OK) return rc;
+    const unsigned char* in = static_cast<const unsigned char*>(src);
+    unsigned char* out = static_cast<unsigned char*>(dst);
+    // DMA chunk c into buffer c & 1, then copy chunk c - 1 out on the host
+    // (the host copy of chunk c - 2 from buffer c & 1 finished before)
+    size_t prev_off = 0, prev_n = 0;
+    int c = 0;
+    for (size_t off = 0; off < bytes; off += kChunk, ++c) {
+        const size_t n = std::min(kChunk, bytes - off);
+        const int b = c & 1;
+        STAGE_TRY(hipMemcpyAsync(pin_[b], in + off, n, hipMemcpyDeviceToHost, s), "hipMemcpyAsync D2H");
+        STAGE_TRY(hipEventRecord(ev_[b], s), "hipEventRecord");
+        if (c >= 1) {
+            STAGE_TRY(hipEventSynchronize(ev_[b ^ 1]), "hipEventSynchronize");
+            pool_->copy(out + prev_off, pin_[b ^ 1], prev_n);
+        }
+        prev_off = off;
+        prev_n = n;
+    }
+    if (c >= 1) {
+        const int b = (c - 1) & 1;
+        STAGE_TRY(hipEventSynchronize(ev_[b]), "hipEventSynchronize");
+        pool_->copy(out + prev_off, pin_[b], prev_n);
+    }
+    return NOMAS_OK;
+}
+
+#undef STAGE_TRY
+
+}  // namespace nomas

@@ -118,7 +118,7 @@ MoeLayer::MoeLayer(DenseTag, int64_t dim, int64_t hidden, DType dt, int device)
 MoeLayer::~MoeLayer() {
     DeviceGuard g(device_);
     free_workspace();
-    for (void* p : {d_wr_, d_w1_, (void*)d_b1_, d_w2_, (void*)d_b2_})
+    for (void* p : {d_wr_, d_w1_, (void*)d_b1_, d_w2_, (void*)d_b2_, d_hio_})
         if (p) (void)hipFree(p);
     for (hipEvent_t e : events_) (void)hipEventDestroy(e);
     if (done_) (void)hipEventDestroy(done_);
@@ -592,23 +592,21 @@ int MoeLayer::forward_host(const void* x, void* y, int64_t rows) {
     DeviceGuard g(device_);
     if (!g.ok) return set_error(NOMAS_ERR_HIP, "hipSetDevice(%d) failed", device_);
     const size_t bytes = (size_t)(rows * D_) * dtype_size(dt_);
-    void *dx = nullptr, *dy = nullptr;
-    HIP_TRY(hipMalloc(&dx, bytes));
-    hipError_t e = hipMalloc(&dy, bytes);
-    if (e != hipSuccess) {
-        (void)hipFree(dx);
-        return set_error(NOMAS_ERR_OUT_OF_MEMORY, "hipMalloc of the output failed: %s", hipGetErrorString(e));
+    // device copies of x and y live with the handle: an allocation and a
+    // free per call cost more than the copies
+    if (bytes > hio_bytes_) {
+        const size_t half = align256(std::max(bytes, hio_bytes_ + hio_bytes_ / 2));
+        if (d_hio_) HIP_TRY(hipFree(d_hio_));
+        d_hio_ = nullptr;
+        hio_bytes_ = 0;
+        HIP_TRY(hipMalloc(&d_hio_, 2 * half));
+        hio_bytes_ = half;
     }
-    int rc = NOMAS_OK;
-    e = hipMemcpy(dx, x, bytes, hipMemcpyHostToDevice);
-    if (e != hipSuccess) rc = set_error(NOMAS_ERR_HIP, "hipMemcpy H2D failed: %s", hipGetErrorString(e));
+    void* dx = d_hio_;
+    void* dy = static_cast<uint8_t*>(d_hio_) + hio_bytes_;
+    int rc = stager_.to_device(dx, x, bytes, nullptr);
     if (rc == NOMAS_OK) rc = forward(dx, dy, rows, nullptr);
-    if (rc == NOMAS_OK) {
-        e = hipMemcpy(y, dy, bytes, hipMemcpyDeviceToHost);
-        if (e != hipSuccess) rc = set_error(NOMAS_ERR_HIP, "hipMemcpy D2H failed: %s", hipGetErrorString(e));
-    }
-    (void)hipFree(dx);
-    (void)hipFree(dy);
+    if (rc == NOMAS_OK) rc = stager_.to_host(y, dy, bytes, nullptr);
     return rc;
 }
 

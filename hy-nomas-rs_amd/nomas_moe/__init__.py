@@ -51,6 +51,14 @@ class DataType(enum.IntEnum):
         return {"f32": cls.F32, "bf16": cls.Bf16, "f16": cls.F16}[str(dt).lower()]
 
 
+def _new_output(xc):
+    """An output like xc: on the GPU for a GPU input; pinned for a host input,
+    so that the result is copied straight back (torch caches pinned blocks)."""
+    if not xc.is_cuda and torch.cuda.is_available():
+        return torch.empty(xc.shape, dtype=xc.dtype, pin_memory=True)
+    return torch.empty_like(xc)
+
+
 class NomasError(RuntimeError):
     """A failed call into the library; ``code`` is the nomas_status value."""
 
@@ -331,7 +339,7 @@ class MoeLayer:
         xc = x.contiguous()
         rows = xc.numel() // self.dim
         if out is None:
-            out = torch.empty_like(xc)
+            out = _new_output(xc)
         L = _lib.lib()
         if xc.is_cuda:
             stream = torch.cuda.current_stream(xc.device).cuda_stream
@@ -467,7 +475,7 @@ class FeedForward:
         xc = x.contiguous()
         rows = xc.numel() // self.dim
         if out is None:
-            out = torch.empty_like(xc)
+            out = _new_output(xc)
         L = _lib.lib()
         if xc.is_cuda:
             stream = torch.cuda.current_stream(xc.device).cuda_stream

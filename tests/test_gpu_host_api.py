@@ -50,6 +50,19 @@ def test_host_tensor_forward_equals_device_forward():
     assert torch.equal(yd, yh)
 
 
+def test_host_tensor_forward_in_several_staging_chunks():
+    # 33,333 rows x 264 f32 = 35.2 MB each way: three 16 MB staging chunks, the
+    # last one partial and not a multiple of 64 bytes, each split over the copy
+    # threads; then a small call on the same handle
+    t, x = small_case(33_333, 264, 4, 1, 96, 32)
+    layer = layer_from_tensors(t, "f32", 264, 96, 4, 1)
+    xd = to_device(x, "f32")
+    yd = layer.forward(xd).cpu()
+    yh = layer.forward(xd.cpu())
+    assert torch.equal(yd, yh)
+    assert torch.equal(layer.forward(xd[:5].cpu()), yd[:5])
+
+
 @pytest.mark.parametrize("src_dtype,model", [(np.float32, "bf16"), (np.float16, "f16"),
                                              (np.float32, "f32")])
 def test_safetensors_checkpoint_equals_in_memory_tensors(tmp_path, src_dtype, model):
