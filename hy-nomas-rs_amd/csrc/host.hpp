@@ -56,6 +56,7 @@ public:
 
 private:
     int ensure();
+    void release();
     void* pin_[2] = {nullptr, nullptr};
     hipEvent_t ev_[2] = {nullptr, nullptr};
     std::unique_ptr<CopyPool> pool_;

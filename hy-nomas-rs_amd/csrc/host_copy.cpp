@@ -91,23 +91,35 @@ bool is_pinned(const void* p) {
     return at.type == hipMemoryTypeHost;
 }
 
-HostStager::~HostStager() {
+HostStager::~HostStager() { release(); }
+
+void HostStager::release() {
     for (int b = 0; b < 2; ++b) {
         if (ev_[b]) (void)hipEventDestroy(ev_[b]);
         if (pin_[b]) (void)hipHostFree(pin_[b]);
+        ev_[b] = nullptr;
+        pin_[b] = nullptr;
     }
+    pool_.reset();
 }
 
+// All or nothing: a failed set-up leaves nothing behind, and the next call tries again.
 int HostStager::ensure() {
-    if (pin_[0]) return NOMAS_OK;
+    if (pool_) return NOMAS_OK;
     for (int b = 0; b < 2; ++b) {
         hipError_t e = hipHostMalloc(&pin_[b], kChunk, hipHostMallocDefault);
-        if (e != hipSuccess)
+        if (e != hipSuccess) {
+            pin_[b] = nullptr;
+            release();
             return set_error(NOMAS_ERR_OUT_OF_MEMORY, "hipHostMalloc of a staging buffer failed: %s",
                              hipGetErrorString(e));
+        }
         e = hipEventCreateWithFlags(&ev_[b], hipEventDisableTiming);
-        if (e != hipSuccess)
+        if (e != hipSuccess) {
+            ev_[b] = nullptr;
+            release();
             return set_error(NOMAS_ERR_HIP, "hipEventCreate failed: %s", hipGetErrorString(e));
+        }
     }
     const unsigned hw = std::thread::hardware_concurrency();
     pool_.reset(new CopyPool((int)std::min(7u, hw > 2 ? hw / 2 - 1 : 0u)));
