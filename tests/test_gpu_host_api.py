@@ -58,8 +58,11 @@ def test_host_tensor_forward_in_several_staging_chunks():
     layer = layer_from_tensors(t, "f32", 264, 96, 4, 1)
     xd = to_device(x, "f32")
     yd = layer.forward(xd).cpu()
-    yh = layer.forward(xd.cpu())
+    yh = layer.forward(xd.cpu())  # pageable in (staged), pinned out (direct)
     assert torch.equal(yd, yh)
+    yp = torch.empty_like(yd)  # pageable out: staged on the way back too
+    layer.forward(xd.cpu(), out=yp)
+    assert torch.equal(yd, yp)
     assert torch.equal(layer.forward(xd[:5].cpu()), yd[:5])
 
 
