@@ -262,8 +262,9 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
 // in ascending expert order (then the dense slot), accumulated in f32.  The
 // row's positions and gates are read once (lane j holds slot j) and broadcast
 // with readlane; each lane has up to 4 slots' loads of its chunks in flight
-// together.
-template <typename T>
+// together.  kResid: the block's gated residual out = x + y * gate
+// (block.rs:101), its x and gate loaded with the first slots' loads.
+template <typename T, bool kResid>
 __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + wave;
@@ -276,15 +277,18 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     T* out = static_cast<T*>(a.out);
     const int my_p = lane < k ? a.tok_pos[row * k + lane] : -1;
     const float my_w = lane < k ? a.topk_w[row * k + lane] : 0.0f;
-    // gated residual: the row's gate and input (block.rs:101)
-    const float* grow = a.gate ? a.gate + row / a.seq * a.D : nullptr;
-    const T* xrow = a.gate ? static_cast<const T*>(a.resid_x) + row * a.D : nullptr;
+    // gated residual: the row's gate and input
+    const float* grow = kResid ? a.gate + row / a.seq * a.D : nullptr;
+    const T* xrow = kResid ? static_cast<const T*>(a.resid_x) + row * a.D : nullptr;
     for (int c0 = lane; c0 < nchunk; c0 += kWave * kBatch) {
-        float acc[kBatch][EPC], xv[kBatch][EPC];
+        float acc[kBatch][EPC], xv[kBatch][EPC], gv[kBatch][EPC];
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) {
             const int c = min(c0 + u * kWave, nchunk - 1);  // past the end: not stored
-            if (grow) load16(xrow + (int64_t)c * EPC, xv[u]);  // in flight with the y loads
+            if constexpr (kResid) {
+                load16(xrow + (int64_t)c * EPC, xv[u]);
+                load_f32s<EPC>(grow + (int64_t)c * EPC, gv[u]);
+            }
 #pragma unroll
             for (int i = 0; i < EPC; ++i) acc[u][i] = 0.0f;
         }
@@ -341,13 +345,11 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
         for (int u = 0; u < kBatch; ++u) {
             const int c = c0 + u * kWave;
             if (c >= nchunk) continue;
-            if (grow) {  // out = x + y * gate, y and each step rounded to the model dtype
-                float g[EPC];
-                load_f32s<EPC>(grow + (int64_t)c * EPC, g);
+            if constexpr (kResid) {  // y and each step rounded to the model dtype
 #pragma unroll
                 for (int i = 0; i < EPC; ++i)
                     acc[u][i] = seam_residual<T>(xv[u][i], Elt<T>::to_f32(Elt<T>::from_f32(acc[u][i])),
-                                                 g[i]);
+                                                 gv[u][i]);
             }
             store16(out + row * a.D + (int64_t)c * EPC, acc[u]);
         }
@@ -405,7 +407,10 @@ hipError_t launch_dispatch_t(const DispatchArgs& a, hipStream_t s) {
 template <typename T>
 hipError_t launch_combine_t(const CombineArgs& a, hipStream_t s) {
     const int nblk = (int)((a.rows + 3) / 4);
-    hipLaunchKernelGGL(combine_kernel<T>, dim3(nblk), dim3(256), 0, s, a);
+    if (a.gate)
+        hipLaunchKernelGGL((combine_kernel<T, true>), dim3(nblk), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((combine_kernel<T, false>), dim3(nblk), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
