@@ -56,7 +56,7 @@ __host__ __device__ inline bool dispatch_fits(int E_cols, int k) {
 //     bytes per K-block; row-major, whole 512-byte slab rows.  Producers and
 //     consumers run separate loops with the same barriers, so neither waits
 //     on the other's memory operations.
-template <typename T>
+template <typename T, bool kKBlocked>
 __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) {
     extern __shared__ __align__(16) unsigned char s_raw[];
     const int Ec = a.E_cols, k = a.k_slots, nch = a.nchunks, b = blockIdx.x;
@@ -234,7 +234,7 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
             const unsigned char* sb = slab + (sl & 1) * kRouterRows * kSlabStride;
             for (int v = ct; v < npieces; v += kDispThreads - kProdThreads) {
                 int pr, h;
-                if (a.kblocked) {  // (K-block, slot, piece): runs along positions
+                if constexpr (kKBlocked) {  // (K-block, slot, piece): runs along positions
                     const int per_kb = npairs * kPPK;
                     const int kbl = v / per_kb, rem = v - kbl * per_kb;
                     pr = rem / kPPK;
@@ -248,7 +248,7 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
                 if (c >= nck || p < 0 || p >= a.a_cap) continue;
                 const uint4 val = *reinterpret_cast<const uint4*>(sb + s_prow[pr] * kSlabStride + h * 16);
                 const int64_t col = (int64_t)c * EPC;
-                const int64_t off = a.kblocked
+                const int64_t off = kKBlocked
                     ? ((col / KB) * a.a_cap + p) * KB + col % KB
                     : (int64_t)p * a.D + col;
                 *reinterpret_cast<uint4*>(xp + off) = val;
@@ -397,10 +397,12 @@ hipError_t launch_dispatch_t(const DispatchArgs& a, hipStream_t s) {
         a.k_slots > a.E_cols || a.BM < 1 || !dispatch_fits(a.E_cols, a.k_slots))
         return hipErrorInvalidValue;
     const size_t lds = dispatch_lds(a.E_cols, a.k_slots);
-    hipError_t err = hipFuncSetAttribute((const void*)dispatch_kernel<T>,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    // the x_perm layout as a compile-time choice: no layout test in the copy loop
+    auto kern = a.kblocked ? dispatch_kernel<T, true> : dispatch_kernel<T, false>;
+    hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         (int)lds);
     if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(dispatch_kernel<T>, dim3(nblk), dim3(kDispThreads), lds, s, a);
+    hipLaunchKernelGGL(kern, dim3(nblk), dim3(kDispThreads), lds, s, a);
     return hipGetLastError();
 }
 
