@@ -197,3 +197,44 @@ def test_dense_ffn_block_composition():
     y = O.round_dt(O.ffn(h0, ff).astype(np.float32), "bf16")
     ref = O.gated_residual(xm, y, g, S, "bf16")
     assert rel_err(out.reshape(B * S, D).float().cpu().numpy(), ref) <= TOL["bf16"]
+
+
+def test_block_and_plain_forwards_interleaved_with_regrowth():
+    # plain forward (small), fused block (larger: the workspace regrows and adds
+    # room for h), plain again (smaller), block again: each call against its
+    # own reference; the handle keeps working across layouts
+    B, D, E, k, H, dtype = 2, 256, 8, 2, 128, "bf16"
+    layer, x, xm, sh, sc, g, nw, p, _ = block_case(B, 400, D, E, k, H, dtype, seed=66)
+    xd = to_device(x, dtype)
+    for S, mode in ((50, "plain"), (400, "block"), (20, "plain"), (300, "block")):
+        print(f"interleaved {mode} S={S}", flush=True)
+        if mode == "plain":
+            rows = B * S
+            y = layer.forward(xd[:rows]).float().cpu().numpy()
+            ref, _, _, _ = O.forward_sparse(xm[:rows], p, k)
+            o_idx, o_w, _, o_gap = O.route(xm[:rows], p["wr"], k)
+        else:
+            xs = np.concatenate([x[b * 400:b * 400 + S] for b in range(B)])
+            xms = np.concatenate([xm[b * 400:b * 400 + S] for b in range(B)])
+            rows = B * S
+            y = layer.forward_block(to_device(xs, dtype).reshape(B, S, D), dev(sh), dev(sc),
+                                    dev(g), dev(nw)).reshape(rows, D).float().cpu().numpy()
+            ref, _, _, _ = O.block_ffn(xms, p, k, sh, sc, g, S, nw, 1e-6, dtype, pow_mode=0)
+            h1, _ = O.norm_modulate(xms, sh, sc, S, nw, 1e-6, dtype, pow_mode=1)
+            o_idx, o_w, _, o_gap = O.route(h1, p["wr"], k)
+        near = check_routing(layer, rows, o_idx, o_w, o_gap, E)
+        assert np.isfinite(y).all() and rel_err(y[~near], ref[~near]) <= TOL[dtype]
+
+
+def test_two_handles_alternating_on_one_stream():
+    # two layers of different shapes used in turn: each has its own workspace
+    l1, x1, xm1, *_, p1, _ = block_case(1, 300, 256, 8, 2, 128, "bf16", seed=67)
+    l2, x2, xm2, *_, p2, _ = block_case(1, 500, 512, 4, 1, 256, "bf16", seed=68)
+    x1d, x2d = to_device(x1, "bf16"), to_device(x2, "bf16")
+    outs = []
+    for _ in range(2):
+        outs.append((l1.forward(x1d).float().cpu().numpy(), l2.forward(x2d).float().cpu().numpy()))
+    for (a, b) in outs:
+        assert rel_err(a, O.forward_sparse(xm1, p1, 2)[0]) <= TOL["bf16"]
+        assert rel_err(b, O.forward_sparse(xm2, p2, 1)[0]) <= TOL["bf16"]
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
