@@ -120,7 +120,10 @@ int nomas_moe_forward_block(nomas_moe_t *h, const void *x, void *out, int64_t ro
                             const float *scale, const float *gate, void *stream);
 
 /* MoeLayer::forward on host tensors (the candle CPU-tensor case): copies x in,
- * runs the forward, copies y out and synchronises. */
+ * runs the forward, copies y out and synchronises.  Pageable buffers are
+ * staged through the handle's pinned buffers (a threaded host copy overlapping
+ * the DMA); pinned buffers (hipHostMalloc'd) go straight to DMA.  The device
+ * copies of x and y stay with the handle between calls. */
 int nomas_moe_forward_host(nomas_moe_t *h, const void *x, void *y, int64_t rows);
 
 /* MoeLayer::n_params (moe.rs:112-114): router + experts, dense excluded. */
