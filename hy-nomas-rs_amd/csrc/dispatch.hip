@@ -261,7 +261,7 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
 // One wave per row: out[row] = sum_j w_j * y_perm[pos_j] over the row's slots
 // in ascending expert order (then the dense slot), accumulated in f32.  The
 // row's positions and gates are read once (lane j holds slot j) and broadcast
-// with readlane; each lane has up to 4 slots' loads of its chunks in flight
+// with readlane; each lane has up to 8 slots' loads of its chunks in flight
 // together.  kResid: the block's gated residual out = x + y * gate
 // (block.rs:101), its x and gate loaded with the first slots' loads.
 template <typename T, bool kResid>
@@ -333,6 +333,7 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
         using Lanes = std::true_type;
         const int k1 = min(k, kWave);
         int j0 = 0;
+        for (; j0 + 8 <= k1; j0 += 8) slots(std::integral_constant<int, 8>{}, Lanes{}, j0);
         for (; j0 + 4 <= k1; j0 += 4) slots(std::integral_constant<int, 4>{}, Lanes{}, j0);
         switch (k1 - j0) {
             case 3: slots(std::integral_constant<int, 3>{}, Lanes{}, j0); break;
