@@ -93,6 +93,18 @@ def test_random_block_configuration(B, S, D, E, k, H, dt, s, affine, seed):
     assert np.isfinite(got).all() and err <= TOL[dt]
 
 
+@pytest.mark.parametrize("B,S,D,E,k,H,dt,s,affine,seed", [
+    (2, 64, 512, 16, 8, 128, "bf16", 0.0, True, 4100),   # one group of 8 slots
+    (1, 300, 256, 40, 10, 256, "f16", 0.5, False, 4101),  # 8 + 3 (dense slot)
+    (3, 17, 512, 64, 8, 128, "f32", 0.5, True, 4102),    # 8 + 1 (dense slot)
+    (1, 64, 264, 17, 9, 96, "bf16", 0.0, True, 4103),    # 8 + 1, general GEMM path
+])
+def test_block_many_slots(B, S, D, E, k, H, dt, s, affine, seed):
+    """forward_block with 8 or more slots per row: the gated-residual combine
+    sums its slots in groups of up to 8."""
+    test_random_block_configuration(B, S, D, E, k, H, dt, s, affine, seed)
+
+
 def _ffn_cases(seed=20261204, n=8):
     rng = random.Random(seed)
     return [(rng.choice([1, 33, 256, 700, 2000]), rng.choice([64, 72, 256, 512]),
