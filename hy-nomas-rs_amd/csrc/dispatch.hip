@@ -23,6 +23,8 @@ constexpr int kSlabBytes = 512;                // bytes of a row per slab
 constexpr int kSlabStride = kSlabBytes + 16;   // LDS row, padded
 constexpr int kSlabPieces = kSlabBytes / 16;   // 16-byte pieces per row per slab
 constexpr int kProdThreads = kDispThreads / 2; // waves 0-7 load, waves 8-15 store
+constexpr int kDispCUs = 256;                  // MI355X compute units
+constexpr int kDispMaxParts = 8;               // blocks sharing one chunk, at most
 constexpr int kProdLoads = kRouterRows * kSlabPieces / kProdThreads;  // 4
 static_assert(kProdLoads * kProdThreads == kRouterRows * kSlabPieces, "whole slabs");
 
@@ -59,7 +61,10 @@ __host__ __device__ inline bool dispatch_fits(int E_cols, int k) {
 template <typename T, bool kKBlocked>
 __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) {
     extern __shared__ __align__(16) unsigned char s_raw[];
-    const int Ec = a.E_cols, k = a.k_slots, nch = a.nchunks, b = blockIdx.x;
+    // parts > 1: blocks b * parts .. b * parts + parts - 1 share chunk b, each
+    // doing the bookkeeping and copying its own contiguous range of slabs
+    const int Ec = a.E_cols, k = a.k_slots, nch = a.nchunks;
+    const int parts = gridDim.x / nch, b = blockIdx.x / parts, part = blockIdx.x % parts;
     unsigned char* slab = s_raw;                   // [2][64][kSlabStride] (step 4)
     int* s_red = reinterpret_cast<int*>(s_raw);    // [2][16][Ec] (steps 1-2)
     int* s_idx = s_red + 2 * kDispWaves * Ec;      // [64 k] the chunk's expert slots (steps 1-3)
@@ -134,7 +139,7 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
         }
     }
     __syncthreads();
-    if (b == 0) {
+    if (b == 0 && part == 0) {
         for (int e = tid; e < Ec; e += kDispThreads) {
             a.expert_count[e] = s_tot[e];
             a.expert_off[e] = s_off[e];
@@ -172,7 +177,7 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
                 const int li = s_lb[e] + rank;
                 s_prow[li] = lane;
                 s_ppos[li] = p;
-                a.tok_pos[(row0 + lane) * k + cur] = p;
+                if (part == 0) a.tok_pos[(row0 + lane) * k + cur] = p;
                 ++cur;
             }
         }
@@ -184,7 +189,10 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
     constexpr int kPPK = kKBlockBytes / 16;  // pieces of one row in one K-block
     static_assert(kSlabPieces % kPPK == 0, "a slab holds whole K-blocks");
     const int nck = a.D / EPC;  // 16-byte chunks per row (D % 8 == 0)
-    const int nslab = (nck + kSlabPieces - 1) / kSlabPieces;
+    const int nslab_all = (nck + kSlabPieces - 1) / kSlabPieces;
+    const int per_part = (nslab_all + parts - 1) / parts;
+    const int sl0 = min(part * per_part, nslab_all);        // this block's first slab
+    const int nslab = min(per_part, nslab_all - sl0);       // and its count (may be 0)
     const int npairs = s_lb[Ec];
     const T* __restrict__ x = static_cast<const T*>(a.x);  // x_perm is the layer's own buffer
     T* __restrict__ xp = static_cast<T*>(a.x_perm);
@@ -195,7 +203,7 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
         auto fetch = [&](int sl, int u) {  // unconditional: clamped to a valid chunk
             const int q = tid + u * kProdThreads;
             const int r = min(q / kSlabPieces, nvalid - 1);
-            const int c = min(sl * kSlabPieces + q % kSlabPieces, nck - 1);
+            const int c = min((sl0 + sl) * kSlabPieces + q % kSlabPieces, nck - 1);
             return *reinterpret_cast<const uint4*>(x + (row0 + r) * (int64_t)a.D + (int64_t)c * EPC);
         };
         auto stash = [&](int buf, int u, const uint4& v) {
@@ -243,7 +251,7 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
                     pr = v / kSlabPieces;
                     h = v % kSlabPieces;
                 }
-                const int c = sl * kSlabPieces + h;
+                const int c = (sl0 + sl) * kSlabPieces + h;
                 const int p = s_ppos[pr];
                 if (c >= nck || p < 0 || p >= a.a_cap) continue;
                 const uint4 val = *reinterpret_cast<const uint4*>(sb + s_prow[pr] * kSlabStride + h * 16);
@@ -403,7 +411,12 @@ hipError_t launch_dispatch_t(const DispatchArgs& a, hipStream_t s) {
     hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                          (int)lds);
     if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(kern, dim3(nblk), dim3(kDispThreads), lds, s, a);
+    // several blocks per chunk when the chunks alone would leave CUs idle
+    // (the copy splits by slabs, the bookkeeping is repeated), as long as the
+    // grid stays within one block per CU: more blocks than CUs measured slower
+    const int nslab = (int)((a.D * sizeof(T) + kSlabBytes - 1) / kSlabBytes);
+    const int parts = std::max(1, std::min({kDispCUs / nblk, nslab, kDispMaxParts}));
+    hipLaunchKernelGGL(kern, dim3(nblk * parts), dim3(kDispThreads), lds, s, a);
     return hipGetLastError();
 }
 
