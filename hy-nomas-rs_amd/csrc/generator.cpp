@@ -76,11 +76,20 @@ void randn_affine(uint64_t seed, double mean, double std, int64_t n, float* out)
     }
     std::vector<std::thread> th;
     const int64_t per = (pairs + nt - 1) / nt;
-    for (unsigned t = 0; t < nt; ++t) {
-        const int64_t p0 = (int64_t)t * per, p1 = std::min<int64_t>(pairs, p0 + per);
-        if (p0 >= p1) break;
-        th.emplace_back(randn_range, seed, mean, std, n, out, p0, p1);
+    int64_t done = 0;  // pairs [0, done) are handed to threads
+    try {
+        th.reserve(nt);
+        for (unsigned t = 0; t < nt; ++t) {
+            const int64_t p0 = (int64_t)t * per, p1 = std::min<int64_t>(pairs, p0 + per);
+            if (p0 >= p1) break;
+            th.emplace_back(randn_range, seed, mean, std, n, out, p0, p1);
+            done = p1;
+        }
+    } catch (...) {
+        // no thread (or no memory) for the rest: this thread draws it; the
+        // values do not depend on who draws them
     }
+    if (done < pairs) randn_range(seed, mean, std, n, out, done, pairs);
     for (auto& x : th) x.join();
 }
 

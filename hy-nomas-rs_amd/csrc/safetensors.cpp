@@ -1,10 +1,26 @@
 // Minimal safetensors reader for the MoE parameters (the format candle's
-// safetensors::load reads in weights.rs:113-116): an 8-byte little-endian
+// safetensors::load reads in weights.rs:113-116, through the `safetensors`
+// crate 0.7 pinned by nomas-core/Cargo.toml:11): an 8-byte little-endian
 // header length, a JSON header mapping tensor names to
 // {"dtype", "shape", "data_offsets": [begin, end]}, then the payload.
-// Only the requested tensors are read from disk.
+//
+// The whole header is validated before anything is allocated for a tensor,
+// following the format's published rules: the header is at most 100,000,000
+// bytes and fits in the file; every entry has a known dtype, non-negative
+// dims whose element count times the dtype size neither overflows nor
+// differs from end - begin; and the entries tile the payload exactly, in
+// offset order, with no hole and no overlap ("the byte buffer needs to be
+// entirely indexed, and cannot contain holes").  Any violation is
+// NOMAS_ERR_IO with the message "loading <path>: <reason>", the form of
+// load_dit's error (weights.rs:112-115).  Only the requested tensors are
+// read from disk.
+#include <sys/types.h>
+
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
+#include <memory>
+#include <utility>
 
 #include "host.hpp"
 
@@ -27,7 +43,10 @@ public:
         ws();
         if (!eat('{')) return false;
         ws();
-        if (eat('}')) return true;
+        if (eat('}')) {
+            ws();
+            return p_ == s_.size();
+        }
         for (;;) {
             std::string key;
             ws();
@@ -44,7 +63,10 @@ public:
             }
             ws();
             if (eat(',')) continue;
-            if (eat('}')) return true;
+            if (eat('}')) {
+                ws();  // the header may be padded with whitespace, nothing else
+                return p_ == s_.size();
+            }
             return false;
         }
     }
@@ -90,7 +112,12 @@ private:
         if (q < s_.size() && s_[q] == '-') { neg = true; ++q; }
         if (q >= s_.size() || s_[q] < '0' || s_[q] > '9') return false;
         int64_t x = 0;
-        while (q < s_.size() && s_[q] >= '0' && s_[q] <= '9') x = x * 10 + (s_[q++] - '0');
+        while (q < s_.size() && s_[q] >= '0' && s_[q] <= '9') {
+            if (__builtin_mul_overflow(x, (int64_t)10, &x) ||
+                __builtin_add_overflow(x, (int64_t)(s_[q] - '0'), &x))
+                return false;  // beyond int64: no valid dim or offset
+            ++q;
+        }
         p_ = q;
         *v = neg ? -x : x;
         return true;
@@ -177,58 +204,110 @@ int64_t dtype_bytes(const std::string& d) {
 
 }  // namespace
 
+namespace {
+
+struct FileCloser {
+    void operator()(FILE* f) const { std::fclose(f); }
+};
+
+// Checks one header entry on its own: known dtype, non-negative dims and
+// offsets, element count x dtype size == end - begin without overflow.
+// Returns nullptr or what is wrong.
+const char* entry_problem(const Entry& e) {
+    const int64_t eb = dtype_bytes(e.dtype);
+    if (eb < 0) return "unknown dtype";
+    if (e.begin < 0 || e.end < 0) return "missing or negative data_offsets";
+    if (e.end < e.begin) return "data_offsets end before begin";
+    int64_t numel = 1;
+    for (int64_t d : e.shape) {
+        if (d < 0) return "negative dimension";
+        if (__builtin_mul_overflow(numel, d, &numel)) return "element count overflows";
+    }
+    int64_t bytes = 0;
+    if (__builtin_mul_overflow(numel, eb, &bytes)) return "byte size overflows";
+    if (bytes != e.end - e.begin) return "byte size does not match shape and dtype";
+    return nullptr;
+}
+
+// Parses and validates the header of `f` (file `path`); on success fills
+// `entries` and the payload's file offset.
+int read_header(FILE* f, const std::string& path, std::map<std::string, Entry>* entries,
+                int64_t* data0) {
+    constexpr uint64_t kMaxHeader = 100000000;  // the format's header limit
+    if (fseeko(f, 0, SEEK_END) != 0)
+        return set_error(NOMAS_ERR_IO, "loading %s: cannot seek", path.c_str());
+    const int64_t fsize = (int64_t)ftello(f);
+    if (fsize < 8 || fseeko(f, 0, SEEK_SET) != 0)
+        return set_error(NOMAS_ERR_IO, "loading %s: truncated header", path.c_str());
+    uint8_t hb[8];
+    if (std::fread(hb, 1, 8, f) != 8)
+        return set_error(NOMAS_ERR_IO, "loading %s: truncated header", path.c_str());
+    uint64_t hlen = 0;
+    for (int i = 7; i >= 0; --i) hlen = (hlen << 8) | hb[i];
+    if (hlen > kMaxHeader)
+        return set_error(NOMAS_ERR_IO, "loading %s: header too large (%llu bytes)", path.c_str(),
+                         (unsigned long long)hlen);
+    if ((int64_t)hlen > fsize - 8)
+        return set_error(NOMAS_ERR_IO, "loading %s: truncated header", path.c_str());
+    std::string hdr(hlen, '\0');
+    if (hlen > 0 && std::fread(&hdr[0], 1, hlen, f) != hlen)
+        return set_error(NOMAS_ERR_IO, "loading %s: truncated header", path.c_str());
+    Json js(hdr);
+    if (!js.parse_header(entries))
+        return set_error(NOMAS_ERR_IO, "loading %s: malformed safetensors header", path.c_str());
+    const int64_t payload = fsize - 8 - (int64_t)hlen;
+    // every entry well-formed, and together they cover [0, payload) in
+    // offset order with no hole or overlap
+    std::vector<std::pair<std::pair<int64_t, int64_t>, const std::string*>> spans;
+    spans.reserve(entries->size());
+    for (const auto& kv : *entries) {
+        if (const char* why = entry_problem(kv.second))
+            return set_error(NOMAS_ERR_IO, "loading %s: tensor %s: %s", path.c_str(),
+                             kv.first.c_str(), why);
+        spans.push_back({{kv.second.begin, kv.second.end}, &kv.first});
+    }
+    std::sort(spans.begin(), spans.end());
+    int64_t at = 0;
+    for (const auto& sp : spans) {
+        if (sp.first.first != at)
+            return set_error(NOMAS_ERR_IO, "loading %s: tensor %s: data_offsets %s the previous tensor",
+                             path.c_str(), sp.second->c_str(),
+                             sp.first.first < at ? "overlap" : "leave a hole after");
+        at = sp.first.second;
+    }
+    if (at != payload)
+        return set_error(NOMAS_ERR_IO,
+                         "loading %s: tensors cover %lld payload bytes, the file holds %lld",
+                         path.c_str(), (long long)at, (long long)payload);
+    *data0 = 8 + (int64_t)hlen;
+    return NOMAS_OK;
+}
+
+}  // namespace
+
 int read_safetensors(const std::vector<std::string>& files, const std::vector<std::string>& names,
                      std::map<std::string, StTensor>* out) {
     for (const std::string& path : files) {
-        FILE* f = std::fopen(path.c_str(), "rb");
+        std::unique_ptr<FILE, FileCloser> f(std::fopen(path.c_str(), "rb"));
         if (!f) return set_error(NOMAS_ERR_IO, "loading %s: cannot open file", path.c_str());
-        uint8_t hb[8];
-        if (std::fread(hb, 1, 8, f) != 8) {
-            std::fclose(f);
-            return set_error(NOMAS_ERR_IO, "loading %s: truncated header", path.c_str());
-        }
-        uint64_t hlen = 0;
-        for (int i = 7; i >= 0; --i) hlen = (hlen << 8) | hb[i];
-        if (hlen > (1ull << 30)) {
-            std::fclose(f);
-            return set_error(NOMAS_ERR_IO, "loading %s: header too large", path.c_str());
-        }
-        std::string hdr(hlen, '\0');
-        if (std::fread(&hdr[0], 1, hlen, f) != hlen) {
-            std::fclose(f);
-            return set_error(NOMAS_ERR_IO, "loading %s: truncated header", path.c_str());
-        }
         std::map<std::string, Entry> entries;
-        Json js(hdr);
-        if (!js.parse_header(&entries)) {
-            std::fclose(f);
-            return set_error(NOMAS_ERR_IO, "loading %s: malformed safetensors header", path.c_str());
-        }
-        const int64_t data0 = 8 + (int64_t)hlen;
+        int64_t data0 = 0;
+        int rc = read_header(f.get(), path, &entries, &data0);
+        if (rc != NOMAS_OK) return rc;
         for (const std::string& n : names) {
             auto it = entries.find(n);
             if (it == entries.end()) continue;
-            const Entry& e = it->second;
-            const int64_t eb = dtype_bytes(e.dtype);
-            int64_t numel = 1;
-            for (int64_t d : e.shape) numel *= d;
-            if (eb < 0 || e.begin < 0 || e.end - e.begin != numel * eb) {
-                std::fclose(f);
-                return set_error(NOMAS_ERR_IO, "loading %s: bad entry for %s", path.c_str(), n.c_str());
-            }
+            const Entry& e = it->second;  // validated: 0 <= begin <= end <= payload
             StTensor t;
             t.dtype = e.dtype;
             t.shape = e.shape;
             t.data.resize((size_t)(e.end - e.begin));
-            if (std::fseek(f, (long)(data0 + e.begin), SEEK_SET) != 0 ||
-                std::fread(t.data.data(), 1, t.data.size(), f) != t.data.size()) {
-                std::fclose(f);
+            if (fseeko(f.get(), (off_t)(data0 + e.begin), SEEK_SET) != 0 ||
+                std::fread(t.data.data(), 1, t.data.size(), f.get()) != t.data.size())
                 return set_error(NOMAS_ERR_IO, "loading %s: truncated payload of %s", path.c_str(),
                                  n.c_str());
-            }
             (*out)[n] = std::move(t);
         }
-        std::fclose(f);
     }
     return NOMAS_OK;
 }

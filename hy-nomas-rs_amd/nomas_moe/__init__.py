@@ -51,6 +51,24 @@ class DataType(enum.IntEnum):
         return {"f32": cls.F32, "bf16": cls.Bf16, "f16": cls.F16}[str(dt).lower()]
 
 
+def _check_out(out: torch.Tensor, like: torch.Tensor, what: str = "out") -> torch.Tensor:
+    """A caller-supplied output must be exactly what the kernels write: x's
+    shape and dtype, contiguous, and on the same side (the same GPU for a
+    device x, the host for a host x).  Checked before any call into the
+    library, so a bad buffer is an error instead of an out-of-bounds write."""
+    if not isinstance(out, torch.Tensor):
+        raise NomasError(2, f"{what} must be a torch.Tensor, got {type(out).__name__}")
+    if tuple(out.shape) != tuple(like.shape):
+        raise NomasError(2, f"{what}: expected shape {tuple(like.shape)}, got {tuple(out.shape)}")
+    if out.dtype != like.dtype:
+        raise NomasError(2, f"{what}: expected dtype {like.dtype}, got {out.dtype}")
+    if not out.is_contiguous():
+        raise NomasError(2, f"{what} must be contiguous")
+    if out.device != like.device:
+        raise NomasError(2, f"{what} is on {out.device}, the input on {like.device}")
+    return out
+
+
 def _new_output(xc):
     """An output like xc: on the GPU for a GPU input; pinned for a host input,
     so that the result is copied straight back (torch caches pinned blocks)."""
@@ -181,6 +199,8 @@ def norm_modulate(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor,
                                    ("norm_w", norm_w, lambda b, d: (d,))))
     if out is None:
         out = torch.empty_like(xc)
+    else:
+        _check_out(out, xc)
     stream = torch.cuda.current_stream(xc.device).cuda_stream
     _check(_lib.lib().nomas_norm_modulate(int(DataType.of(xc.dtype)), xc.data_ptr(),
                                           out.data_ptr(), B * S, D, max(S, 1), _ptr(nw),
@@ -193,13 +213,15 @@ def gated_residual(x: torch.Tensor, y: torch.Tensor, gate: torch.Tensor,
     """out = x + y * gate (block.rs:101).  x, y: (B, L, D) device tensors of one
     dtype; gate: (B, D)."""
     xc = _seam_input(x)
-    if tuple(y.shape) != tuple(xc.shape) or y.dtype != xc.dtype:
-        raise NomasError(2, "y must match x in shape and dtype")
+    if tuple(y.shape) != tuple(xc.shape) or y.dtype != xc.dtype or y.device != xc.device:
+        raise NomasError(2, "y must match x in shape, dtype and device")
     yc = y.contiguous()
     B, S, D = xc.shape
     (g,) = _seam_params(xc, (("gate", gate, lambda b, d: (b, d)),))
     if out is None:
         out = torch.empty_like(xc)
+    else:
+        _check_out(out, xc)
     stream = torch.cuda.current_stream(xc.device).cuda_stream
     _check(_lib.lib().nomas_gated_residual(int(DataType.of(xc.dtype)), xc.data_ptr(),
                                            yc.data_ptr(), g.data_ptr(), out.data_ptr(), B * S, D,
@@ -340,6 +362,8 @@ class MoeLayer:
         rows = xc.numel() // self.dim
         if out is None:
             out = _new_output(xc)
+        else:
+            _check_out(out, xc)
         L = _lib.lib()
         if xc.is_cuda:
             stream = torch.cuda.current_stream(xc.device).cuda_stream
@@ -369,6 +393,10 @@ class MoeLayer:
                                           ("norm_w", norm_w, lambda b, d: (d,))))
         if out is None:
             out = torch.empty_like(xc)
+        else:
+            # in place on a strided x would compute on a copy and write the
+            # contiguous result over x's strided storage: the check rejects it
+            _check_out(out, xc)
         stream = torch.cuda.current_stream(xc.device).cuda_stream
         _check(_lib.lib().nomas_moe_forward_block(
             self._h, xc.data_ptr(), out.data_ptr(), B * S, max(S, 1), _ptr(nw), float(eps),
@@ -476,6 +504,8 @@ class FeedForward:
         rows = xc.numel() // self.dim
         if out is None:
             out = _new_output(xc)
+        else:
+            _check_out(out, xc)
         L = _lib.lib()
         if xc.is_cuda:
             stream = torch.cuda.current_stream(xc.device).cuda_stream

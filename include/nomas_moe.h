@@ -11,7 +11,10 @@
  *    nomas_moe_last_error().  These map onto the reference's error variants
  *    (nomas-core/src/error.rs:7-46): INVALID_CONFIG -> Error::InvalidConfig,
  *    WEIGHT_KEY -> Error::WeightKey, IO -> Error::Io, everything else ->
- *    Error::Candle / Error::Msg.
+ *    Error::Candle / Error::Msg.  A checkpoint that cannot be read or parsed
+ *    is NOMAS_ERR_IO with the message "loading <path>: <reason>", as
+ *    load_dit maps it (weights.rs:112-115).  No entry point lets a C++
+ *    exception or an abort escape: failures are always a returned status.
  *  - Tensors are row-major.  A forward input of any rank >= 2 with last dim D
  *    is passed as `rows` = product of the leading dims, exactly as Lin::fwd
  *    folds leading dims (nomas-core/src/modules/mod.rs:132-134).
@@ -42,7 +45,8 @@ enum nomas_status {
     NOMAS_ERR_IO = 4,               /* checkpoint file could not be read           */
     NOMAS_ERR_HIP = 5,              /* a HIP runtime call failed                   */
     NOMAS_ERR_OUT_OF_MEMORY = 6,    /* device or host allocation failed            */
-    NOMAS_ERR_STATE = 7             /* e.g. routing read back before any forward   */
+    NOMAS_ERR_STATE = 7,            /* e.g. routing read back before any forward   */
+    NOMAS_ERR_INTERNAL = 8          /* an unexpected failure inside the library    */
 };
 
 /* DataType (config.rs:30-39). */
@@ -109,7 +113,8 @@ int nomas_moe_forward(nomas_moe_t *h, const void *x, void *y, int64_t rows, void
  * DiTBlock::from_source, block.rs:56-57).  Rounding to the model dtype happens
  * where the reference's to_dtype casts do (after the norm, after modulate, on
  * the MoE output, on y * gate and on the sum); the row's sum of squares is
- * accumulated in f64.  For an F32 handle this is the reference's arithmetic;
+ * the reference's serial f32 chain, one rounded add per element in ascending
+ * column order (norm.rs:58-65).  For an F32 handle this is the reference's arithmetic;
  * for BF16/F16 the reference's modulate (an F32 tensor times model-dtype
  * parameters) does not type-check in candle, and this entry point defines the
  * block with the f32 parameters above.  The router sees h, so routing()

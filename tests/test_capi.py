@@ -254,3 +254,86 @@ def test_ffn_complete_checkpoint_parses_then_needs_a_device(tmp_path):
         assert rc == 0, msg
     else:
         assert rc == 5 and "HIP device" in msg
+
+
+# ---- malformed checkpoints: always NOMAS_ERR_IO "loading <path>: ...", never an abort
+# (load_dit maps every unreadable file to Error::Msg("loading {path}: {e}"),
+# weights.rs:112-115; the format rules are the safetensors crate's, Cargo.toml:11)
+
+def _raw_safetensors(path, entries, payload=b"", pad=b""):
+    """Writes a file with a hand-made header: entries maps name -> dict."""
+    import json
+    hdr = json.dumps(entries).encode() + pad
+    with open(path, "wb") as f:
+        f.write(len(hdr).to_bytes(8, "little"))
+        f.write(hdr)
+        f.write(payload)
+
+
+_MALFORMED = {
+    # the advisor's case: a negative dim and end < begin agree in "size" (-4 == -4)
+    "negative_shape": ({"t": {"dtype": "F32", "shape": [-1], "data_offsets": [4, 0]}}, b"\0" * 4),
+    "end_before_begin": ({"t": {"dtype": "F32", "shape": [1], "data_offsets": [8, 4]}}, b"\0" * 8),
+    "end_past_eof": ({"t": {"dtype": "F32", "shape": [1024], "data_offsets": [0, 4096]}}, b"\0" * 16),
+    "huge_shape": ({"t": {"dtype": "F32", "shape": [2 ** 62], "data_offsets": [0, 2 ** 62 * 4 % 2 ** 63]}},
+                   b""),
+    "numel_overflow": ({"t": {"dtype": "BF16", "shape": [2 ** 40, 2 ** 40], "data_offsets": [0, 0]}},
+                       b""),
+    "offset_beyond_int64": ({"t": {"dtype": "F32", "shape": [1],
+                                   "data_offsets": [0, 99999999999999999999999]}}, b"\0" * 4),
+    "size_mismatch": ({"t": {"dtype": "F32", "shape": [3], "data_offsets": [0, 8]}}, b"\0" * 8),
+    "hole": ({"a": {"dtype": "F32", "shape": [1], "data_offsets": [0, 4]},
+              "b": {"dtype": "F32", "shape": [1], "data_offsets": [8, 12]}}, b"\0" * 12),
+    "overlap": ({"a": {"dtype": "F32", "shape": [2], "data_offsets": [0, 8]},
+                 "b": {"dtype": "F32", "shape": [1], "data_offsets": [4, 8]}}, b"\0" * 8),
+    "trailing_bytes": ({"t": {"dtype": "F32", "shape": [1], "data_offsets": [0, 4]}}, b"\0" * 12),
+    "unknown_dtype": ({"t": {"dtype": "Q4", "shape": [1], "data_offsets": [0, 4]}}, b"\0" * 4),
+    "no_offsets": ({"t": {"dtype": "F32", "shape": [1]}}, b"\0" * 4),
+}
+
+
+@pytest.mark.parametrize("case", sorted(_MALFORMED))
+@pytest.mark.parametrize("loader", ["moe", "ffn"])
+def test_malformed_checkpoint_is_an_io_error(tmp_path, case, loader):
+    entries, payload = _MALFORMED[case]
+    f = str(tmp_path / f"{case}.safetensors")
+    _raw_safetensors(f, entries, payload)
+    rc, msg = _load([f]) if loader == "moe" else _load_ffn([f])
+    assert rc == 4, (rc, msg)
+    assert msg.startswith(f"loading {f}: "), msg
+
+
+@pytest.mark.parametrize("loader", ["moe", "ffn"])
+def test_truncated_and_oversized_headers(tmp_path, loader):
+    load = _load if loader == "moe" else _load_ffn
+    short = tmp_path / "short.safetensors"
+    short.write_bytes(b"\x05\x00\x00")  # not even the 8-byte length
+    bigh = tmp_path / "bigh.safetensors"
+    bigh.write_bytes((200_000_000).to_bytes(8, "little") + b"{}")  # beyond the 100 MB limit
+    liar = tmp_path / "liar.safetensors"
+    liar.write_bytes((4096).to_bytes(8, "little") + b"{}")  # header longer than the file
+    junk = tmp_path / "junk.safetensors"
+    _raw_safetensors(str(junk), {}, pad=b"  x")  # non-space after the JSON
+    for p in (short, bigh, liar, junk):
+        rc, msg = load([str(p)])
+        assert rc == 4 and msg.startswith(f"loading {p}: "), (p.name, rc, msg)
+
+
+def test_well_formed_edge_headers_pass_the_parser(tmp_path):
+    # whitespace padding after the JSON, __metadata__, and an empty tensor are
+    # all legal; the checkpoint is then complete and loading reaches the device
+    f = str(tmp_path / "ok.safetensors")
+    t = _checkpoint(f, 2, 16, 8)
+    from safetensors.numpy import load_file
+    back = load_file(f)
+    assert set(back) == set(t)
+    import json
+    raw = open(f, "rb").read()
+    n = int.from_bytes(raw[:8], "little")
+    hdr = json.loads(raw[8:8 + n])
+    hdr["__metadata__"] = {"format": "pt"}
+    hdr["zz.empty"] = {"dtype": "F32", "shape": [0, 3], "data_offsets": [len(raw) - 8 - n] * 2}
+    _raw_safetensors(f, hdr, raw[8 + n:], pad=b"    ")
+    rc, msg = _load([f])
+    import torch
+    assert rc == (0 if torch.cuda.is_available() else 5), msg
