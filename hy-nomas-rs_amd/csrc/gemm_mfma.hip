@@ -331,12 +331,18 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
         // Part of a split tile: publish the partial sums, count arrivals; the
         // last part to arrive adds all parts in part order (the same order
         // whichever part that is, so results do not depend on timing) and
-        // runs the epilogue.  Partials are written and read with agent-scope
-        // coherent accesses (sc1: through to the point of coherence of all
-        // XCDs), and every write has completed (vmcnt 0) before the counter
-        // moves, so no L2-wide write-back or invalidate is needed.  Reads past
-        // the tile's `parts` partials return zero (buffer range check).  The
-        // counter goes back to zero for the next launch.
+        // runs the epilogue.  The parts of one tile run on different XCDs,
+        // whose L2 caches are not coherent with each other.  The hand-off is
+        // a release/acquire pair at agent scope: every part's counter
+        // increment is a release read-modify-write (its partial stores, done
+        // by all threads before the barrier, happen-before it), and the part
+        // whose increment completes the count (reading every other part's
+        // release) runs an agent-scope acquire fence before any partial load.
+        // Only that part pays for the acquire's cache invalidation.  The
+        // partials themselves are written and read with the agent-scope cache
+        // policy (sc1), so they travel past the XCD's L2 instead of through it.
+        // Reads past the tile's `parts` partials return zero (buffer range
+        // check).  The counter goes back to zero for the next launch.
         constexpr int NB = SN * SM;
         static_assert(NB * 4 * kThreads == kSplitUnitFloats, "one unit = one 256 x 256 tile");
         constexpr int kUnitBytes = (int)(kSplitUnitFloats * sizeof(float));
@@ -353,7 +359,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
         wait_vmcnt<0>();
         __shared__ int s_last;
         __syncthreads();
-        if (tid == 0) s_last = atomicAdd(&a.split_cnt[wu.slot], 1) == wu.parts - 1;
+        if (tid == 0) {
+            s_last = __hip_atomic_fetch_add(&a.split_cnt[wu.slot], 1, __ATOMIC_RELEASE,
+                                            __HIP_MEMORY_SCOPE_AGENT) == wu.parts - 1;
+            if (s_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        }
         __syncthreads();
         if (!s_last) return;
         // one weight block at a time: its 8 x kMaxSplit loads all in flight
@@ -376,7 +386,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
                 acc[i][j] = t;
             }
         }
-        if (tid == 0) a.split_cnt[wu.slot] = 0;
+        if (tid == 0)
+            __hip_atomic_store(&a.split_cnt[wu.slot], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
     // Epilogue (the accumulators include the bias).  Lane (l16, lq) of block

@@ -87,6 +87,30 @@ int st_to_f32(const StTensor& t, std::vector<float>* out);
 
 // ---- the layer -----------------------------------------------------------
 
+// Device buffers of one forward, kept by the handle (grown as needed).  The
+// split-tile counters and partials come first, at offsets that do not depend
+// on the row count, so counters left at zero by one forward are where the
+// next one looks for them.
+struct Workspace {
+    int64_t cap_rows = 0;  // rows the buffers are laid out for (a multiple of 64)
+    int32_t* split_cnt = nullptr;    // MFMA path: arrival counters of K-split tiles
+    float* split_ws = nullptr;       // MFMA path: their f32 partial tiles
+    int32_t* idx = nullptr;          // rows x k_slots
+    float* w = nullptr;              // rows x k_slots
+    float* gap = nullptr;            // rows
+    int32_t* pos = nullptr;          // rows x k_slots
+    int32_t* chunk_counts = nullptr; // chunks x E_cols
+    int32_t* expert_count = nullptr; // E_cols
+    int32_t* expert_off = nullptr;   // E_cols + 1
+    TileInfo* tiles = nullptr;       // max_tiles
+    int32_t* tile_total = nullptr;   // 1
+    void* xperm = nullptr;           // a_cap x D
+    void* h = nullptr;               // a_cap x H
+    void* yperm = nullptr;           // a_cap x D (MoE only)
+    void* block_h = nullptr;         // forward_block: rows x D
+};
+
+
 // Parameters of one Lin in f32, reference (out, in) layout.
 struct LinF32 {
     std::vector<float> w;
@@ -157,6 +181,9 @@ private:
     int ensure_workspace(int64_t rows);
     void free_workspace();
     int max_tiles(int64_t rows) const;
+    // Lays out the buffers of a forward on up to `cap` rows (a multiple of
+    // 64) from `base` (nullptr: sizes only) and returns the bytes used.
+    size_t layout(int64_t cap, bool block, uint8_t* base, Workspace* w) const;
 
     int64_t D_, H_, E_, k_;
     int64_t Ecols_, kslots_;  // with the shared dense branch: E + 1, k + 1
@@ -167,7 +194,12 @@ private:
     int BM_;
     bool dense_only_ = false;
     int forward_dense(const void* x, void* y, int64_t rows, hipStream_t s);
+    int check_forward(const void* x, const void* y, int64_t rows) const;
     int forward_impl(const void* x, void* y, int64_t rows, hipStream_t s, const BlockArgs* blk);
+    // the stages of a routed forward on the buffers of `w`
+    int run_routed(const void* x, void* y, int64_t rows, hipStream_t s, const BlockArgs* blk,
+                   const Workspace& w);
+    int finish_forward(int64_t rows, hipStream_t s, const Workspace& w);
     bool want_block_ = false;  // the workspace holds h for forward_block
 
     // device weights
@@ -177,29 +209,17 @@ private:
     void* d_w2_ = nullptr;    // down [Ecols][D][H]
     float* d_b2_ = nullptr;   // [Ecols][D]
 
-    // workspace (sized for cap_rows_)
-    int64_t cap_rows_ = 0;
+    // the handle's workspace (sized for ws_.cap_rows rows)
     void* d_ws_ = nullptr;
+    Workspace ws_;
+    // where the last forward's routing lives: ws_, or the scratch array
+    Workspace last_ws_;
+    bool last_in_scratch_ = false;
     // forward_host: device copies of x and y, kept between calls (grown as
     // needed), and the pinned staging of the copies
     void* d_hio_ = nullptr;
     size_t hio_bytes_ = 0;  // bytes of each of the two halves
     HostStager stager_;
-    int32_t* d_idx_ = nullptr;
-    float* d_w_ = nullptr;
-    float* d_gap_ = nullptr;
-    int32_t* d_pos_ = nullptr;
-    int32_t* d_chunk_counts_ = nullptr;
-    int32_t* d_expert_count_ = nullptr;
-    int32_t* d_expert_off_ = nullptr;
-    TileInfo* d_tiles_ = nullptr;
-    int32_t* d_tile_total_ = nullptr;
-    void* d_xperm_ = nullptr;
-    void* d_h_ = nullptr;
-    void* d_yperm_ = nullptr;
-    void* d_block_h_ = nullptr;       // forward_block: h = modulate(norm2(x)), rows x D
-    float* d_split_ws_ = nullptr;     // MFMA path: partial tiles of K-split GEMM tails
-    int32_t* d_split_cnt_ = nullptr;  // their arrival counters
 
     int64_t last_rows_ = -1;
     hipStream_t last_stream_ = nullptr;

@@ -22,7 +22,8 @@ namespace nomas {
 // ---- errors ---------------------------------------------------------------
 
 namespace {
-thread_local std::string g_last_error;
+// a fixed buffer: recording an error never allocates (or throws)
+thread_local char g_last_error[1024];
 
 struct DeviceGuard {
     int prev = -1;
@@ -47,17 +48,15 @@ constexpr unsigned kDoneFlags = hipEventDisableTiming | hipEventReleaseToDevice;
 }  // namespace
 
 int set_error(int code, const char* fmt, ...) {
-    char buf[1024];
     va_list ap;
     va_start(ap, fmt);
-    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    std::vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
     va_end(ap);
-    g_last_error = buf;
     return code;
 }
 
-const char* last_error() { return g_last_error.c_str(); }
-void clear_error() { g_last_error.clear(); }
+const char* last_error() { return g_last_error; }
+void clear_error() { g_last_error[0] = '\0'; }
 
 #define HIP_TRY(expr)                                                                        \
     do {                                                                                     \
@@ -164,6 +163,8 @@ int MoeLayer::upload(const void* router_w, const void* gate_w, const void* gate_
 
     DeviceGuard g(device_);
     if (!g.ok) return set_error(NOMAS_ERR_HIP, "hipSetDevice(%d) failed", device_);
+    // the end-of-forward event, made here so that no forward creates anything
+    if (!done_) HIP_TRY(hipEventCreateWithFlags(&done_, kDoneFlags));
 
     // gate/up
     std::vector<uint8_t> w1((size_t)(Ecols_ * 2 * H * D) * es);
@@ -282,70 +283,82 @@ int MoeLayer::max_tiles(int64_t rows) const {
     return (int)((A + BM_ - 1) / BM_ + Ecols_);
 }
 
-void MoeLayer::free_workspace() {
-    if (d_ws_) (void)hipFree(d_ws_);
-    d_ws_ = nullptr;
-    d_block_h_ = nullptr;
-    cap_rows_ = 0;
-    last_rows_ = -1;  // the last forward's routing went with the buffers
-}
-
-int MoeLayer::ensure_workspace(int64_t rows) {
-    if (rows <= cap_rows_ && (!want_block_ || d_block_h_)) return NOMAS_OK;
-    int64_t cap = std::max<int64_t>(rows, cap_rows_ + cap_rows_ / 2);
-    cap = (cap + kRouterRows - 1) / kRouterRows * kRouterRows;
+size_t MoeLayer::layout(int64_t cap, bool block, uint8_t* base, Workspace* w) const {
     const int64_t A = cap * kslots_;
     const int64_t nch = cap / kRouterRows;
     const size_t es = dtype_size(dt_);
     const int mt = max_tiles(cap);
     size_t off = 0;
-    auto take = [&](size_t bytes) { size_t o = off; off += align256(bytes); return o; };
-    const size_t o_idx = take(sizeof(int32_t) * A);
-    const size_t o_w = take(sizeof(float) * A);
-    const size_t o_gap = take(sizeof(float) * cap);
-    const size_t o_pos = take(sizeof(int32_t) * A);
-    const size_t o_cc = take(sizeof(int32_t) * nch * Ecols_);
-    const size_t o_ec = take(sizeof(int32_t) * Ecols_);
-    const size_t o_eo = take(sizeof(int32_t) * (Ecols_ + 1));
-    const size_t o_tiles = take(sizeof(TileInfo) * mt);
-    const size_t o_tt = take(sizeof(int32_t));
-    const size_t o_xp = take(es * A * D_);
-    const size_t o_h = take(es * A * H_);
-    const size_t o_yp = dense_only_ ? 0 : take(es * A * D_);  // dense: the down GEMM writes y
-    const size_t o_bh = want_block_ ? take(es * cap * D_) : 0;
-    const size_t o_sw = mfma_ ? take(sizeof(float) * kSplitUnitFloats * kSplitUnits) : 0;
-    const size_t o_sc = mfma_ ? take(sizeof(int32_t) * kSplitUnits) : 0;
+    auto take = [&](size_t bytes) -> uint8_t* {
+        const size_t o = off;
+        off += align256(bytes);
+        return base ? base + o : nullptr;
+    };
+    Workspace v;
+    v.cap_rows = cap;
+    // First, at fixed offsets: the split-tile counters, then the partials.  The
+    // counters' bytes are reserved in every layout (also where no GEMM splits)
+    // so that nothing else ever writes there: in the shared scratch array they
+    // stay zero from one forward to the next, whichever layer ran before.
+    v.split_cnt = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * kSplitUnits));
+    if (mfma_)
+        v.split_ws = reinterpret_cast<float*>(take(sizeof(float) * kSplitUnitFloats * kSplitUnits));
+    v.idx = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * A));
+    v.w = reinterpret_cast<float*>(take(sizeof(float) * A));
+    v.gap = reinterpret_cast<float*>(take(sizeof(float) * cap));
+    v.pos = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * A));
+    v.chunk_counts = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * nch * Ecols_));
+    v.expert_count = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * Ecols_));
+    v.expert_off = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * (Ecols_ + 1)));
+    v.tiles = reinterpret_cast<TileInfo*>(take(sizeof(TileInfo) * mt));
+    v.tile_total = reinterpret_cast<int32_t*>(take(sizeof(int32_t)));
+    v.xperm = take(es * A * D_);
+    v.h = take(es * A * H_);
+    if (!dense_only_) v.yperm = take(es * A * D_);  // dense: the down GEMM writes y
+    if (block) v.block_h = take(es * cap * D_);
+    if (w) *w = v;
+    return off;
+}
+
+void MoeLayer::free_workspace() {
+    if (d_ws_) (void)hipFree(d_ws_);
+    d_ws_ = nullptr;
+    ws_ = Workspace();
+    if (!last_in_scratch_) last_rows_ = -1;  // the last forward's routing went with the buffers
+}
+
+int MoeLayer::ensure_workspace(int64_t rows) {
+    if (rows <= ws_.cap_rows && (!want_block_ || ws_.block_h)) return NOMAS_OK;
+    int64_t cap = std::max<int64_t>(rows, ws_.cap_rows + ws_.cap_rows / 2);
+    cap = (cap + kRouterRows - 1) / kRouterRows * kRouterRows;
+    const size_t bytes = layout(cap, want_block_, nullptr, nullptr);
     free_workspace();
     void* ws = nullptr;
-    HIP_TRY(hipMalloc(&ws, off));
+    HIP_TRY(hipMalloc(&ws, bytes));
     d_ws_ = ws;
+    layout(cap, want_block_, static_cast<uint8_t*>(ws), &ws_);
     if (mfma_) {
         // the split-tile counters start at zero; the GEMMs keep them there.
         // Finished before any stream (blocking or not) can use the workspace.
-        HIP_TRY(hipMemset(static_cast<uint8_t*>(ws) + o_sc, 0, sizeof(int32_t) * kSplitUnits));
+        HIP_TRY(hipMemset(ws_.split_cnt, 0, sizeof(int32_t) * kSplitUnits));
         HIP_TRY(hipDeviceSynchronize());
     }
-    uint8_t* b = static_cast<uint8_t*>(ws);
-    d_idx_ = reinterpret_cast<int32_t*>(b + o_idx);
-    d_w_ = reinterpret_cast<float*>(b + o_w);
-    d_gap_ = reinterpret_cast<float*>(b + o_gap);
-    d_pos_ = reinterpret_cast<int32_t*>(b + o_pos);
-    d_chunk_counts_ = reinterpret_cast<int32_t*>(b + o_cc);
-    d_expert_count_ = reinterpret_cast<int32_t*>(b + o_ec);
-    d_expert_off_ = reinterpret_cast<int32_t*>(b + o_eo);
-    d_tiles_ = reinterpret_cast<TileInfo*>(b + o_tiles);
-    d_tile_total_ = reinterpret_cast<int32_t*>(b + o_tt);
-    d_xperm_ = b + o_xp;
-    d_h_ = b + o_h;
-    d_yperm_ = dense_only_ ? nullptr : b + o_yp;
-    d_block_h_ = want_block_ ? b + o_bh : nullptr;
-    d_split_ws_ = mfma_ ? reinterpret_cast<float*>(b + o_sw) : nullptr;
-    d_split_cnt_ = mfma_ ? reinterpret_cast<int32_t*>(b + o_sc) : nullptr;
-    cap_rows_ = cap;
     return NOMAS_OK;
 }
 
 // ---- forward ------------------------------------------------------------------
+
+int MoeLayer::check_forward(const void* x, const void* y, int64_t rows) const {
+    if (rows < 0) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "rows must be >= 0 (got %lld)", (long long)rows);
+    if (rows == 0) return NOMAS_OK;
+    if (!x || !y) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "x and y must be non-null");
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15)
+        return set_error(NOMAS_ERR_INVALID_ARGUMENT, "x and y must be 16-byte aligned");
+    if (!d_w1_) return set_error(NOMAS_ERR_STATE, "weights have not been uploaded");
+    if (rows * kslots_ > 0x7fffffffLL || rows * kslots_ * std::max(D_, H_) > (1LL << 40))
+        return set_error(NOMAS_ERR_INVALID_ARGUMENT, "rows=%lld exceed the supported range", (long long)rows);
+    return NOMAS_OK;
+}
 
 int MoeLayer::forward(const void* x, void* y, int64_t rows, hipStream_t s) {
     return forward_impl(x, y, rows, s, nullptr);
@@ -370,26 +383,40 @@ int MoeLayer::forward_block(const void* x, void* out, int64_t rows, const BlockA
 
 int MoeLayer::forward_impl(const void* x, void* y, int64_t rows, hipStream_t s,
                            const BlockArgs* blk) {
-    if (rows < 0) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "rows must be >= 0 (got %lld)", (long long)rows);
-    if (rows == 0) { last_rows_ = 0; return NOMAS_OK; }
-    if (!x || !y) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "x and y must be non-null");
-    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15)
-        return set_error(NOMAS_ERR_INVALID_ARGUMENT, "x and y must be 16-byte aligned");
-    if (!d_w1_) return set_error(NOMAS_ERR_STATE, "weights have not been uploaded");
-    if (rows * kslots_ > 0x7fffffffLL || rows * kslots_ * std::max(D_, H_) > (1LL << 40))
-        return set_error(NOMAS_ERR_INVALID_ARGUMENT, "rows=%lld exceed the supported range", (long long)rows);
+    int rc = check_forward(x, y, rows);
+    if (rc != NOMAS_OK) return rc;
+    if (rows == 0) { last_rows_ = 0; last_in_scratch_ = false; return NOMAS_OK; }
     DeviceGuard g(device_);
     if (!g.ok) return set_error(NOMAS_ERR_HIP, "hipSetDevice(%d) failed", device_);
-    int rc = ensure_workspace(rows);
+    rc = ensure_workspace(rows);
     if (rc != NOMAS_OK) return rc;
     if (done_recorded_ && s != last_stream_) HIP_TRY(hipStreamWaitEvent(s, done_, 0));
     if (dense_only_) {
         if (blk) return set_error(NOMAS_ERR_STATE, "the fused block is implemented for the MoE layer");
         return forward_dense(x, y, rows, s);
     }
+    rc = run_routed(x, y, rows, s, blk, ws_);
+    if (rc != NOMAS_OK) return rc;
+    last_in_scratch_ = false;
+    return finish_forward(rows, s, ws_);
+}
 
+int MoeLayer::finish_forward(int64_t rows, hipStream_t s, const Workspace& w) {
+    // done_ is created with the weights; recording it allocates nothing
+    HIP_TRY(hipEventRecord(done_, s));
+    done_recorded_ = true;
+    last_rows_ = rows;
+    last_stream_ = s;
+    last_ws_ = w;
+    return NOMAS_OK;
+}
+
+int MoeLayer::run_routed(const void* x, void* y, int64_t rows, hipStream_t s,
+                         const BlockArgs* blk, const Workspace& w) {
+    int rc;
     const int nch = (int)((rows + kRouterRows - 1) / kRouterRows);
     const int mt = max_tiles(rows);
+    const int64_t a_cap = w.cap_rows * kslots_;
     hipEvent_t* ev = nullptr;
     if (profiling_) {
         ev = &events_[(size_t)(recorded_ % kRing) * 7];
@@ -411,7 +438,7 @@ int MoeLayer::forward_impl(const void* x, void* y, int64_t rows, hipStream_t s,
     if (blk) {
         SeamArgs sm;
         sm.x = x;
-        sm.h = d_block_h_;
+        sm.h = w.block_h;
         sm.rows = rows;
         sm.D = (int)D_;
         sm.seq = blk->seq;
@@ -420,7 +447,7 @@ int MoeLayer::forward_impl(const void* x, void* y, int64_t rows, hipStream_t s,
         sm.shift = blk->shift;
         sm.scale = blk->scale;
         STAGE(launch_seam_h(dt_, sm, s), "norm/modulate");
-        xr = d_block_h_;
+        xr = w.block_h;
     }
     RouterArgs ra;
     ra.x = xr;
@@ -431,10 +458,10 @@ int MoeLayer::forward_impl(const void* x, void* y, int64_t rows, hipStream_t s,
     ra.k = (int)k_;
     ra.k_slots = (int)kslots_;
     ra.dense_coef = (float)shared_dense_;
-    ra.topk_idx = d_idx_;
-    ra.topk_w = d_w_;
-    ra.gap = d_gap_;
-    ra.chunk_counts = d_chunk_counts_;
+    ra.topk_idx = w.idx;
+    ra.topk_w = w.w;
+    ra.gap = w.gap;
+    ra.chunk_counts = w.chunk_counts;
     STAGE(launch_router(dt_, ra, s), "router");
     if ((rc = mark(1))) return rc;
 
@@ -448,45 +475,45 @@ int MoeLayer::forward_impl(const void* x, void* y, int64_t rows, hipStream_t s,
     da.D = (int)D_;
     da.E_cols = (int)Ecols_;
     da.k_slots = (int)kslots_;
-    da.topk_idx = d_idx_;
-    da.chunk_counts = d_chunk_counts_;
+    da.topk_idx = w.idx;
+    da.chunk_counts = w.chunk_counts;
     da.nchunks = nch;
     da.BM = BM_;
     da.max_tiles = mt;
-    da.expert_count = d_expert_count_;
-    da.expert_off = d_expert_off_;
-    da.tiles = d_tiles_;
-    da.tile_total = d_tile_total_;
-    da.tok_pos = d_pos_;
-    da.x_perm = d_xperm_;
-    da.a_cap = cap_rows_ * kslots_;
+    da.expert_count = w.expert_count;
+    da.expert_off = w.expert_off;
+    da.tiles = w.tiles;
+    da.tile_total = w.tile_total;
+    da.tok_pos = w.pos;
+    da.x_perm = w.xperm;
+    da.a_cap = a_cap;
     da.kblocked = mfma_ ? 1 : 0;
     STAGE(launch_dispatch(dt_, da, s), "dispatch");
     if ((rc = mark(3))) return rc;
 
     GemmArgs g1;
-    g1.X = d_xperm_;
+    g1.X = w.xperm;
     g1.W = d_w1_;
     g1.bias = d_b1_;
-    g1.out = d_h_;
-    g1.tiles = d_tiles_;
-    g1.tile_total = d_tile_total_;
+    g1.out = w.h;
+    g1.tiles = w.tiles;
+    g1.tile_total = w.tile_total;
     g1.max_tiles = mt;
     g1.N = (int)(2 * H_);
     g1.K = (int)D_;
     g1.num_experts = (int)Ecols_;
-    g1.a_cap = cap_rows_ * kslots_;
-    g1.split_ws = d_split_ws_;
-    g1.split_cnt = d_split_cnt_;
+    g1.a_cap = a_cap;
+    g1.split_ws = w.split_ws;
+    g1.split_cnt = w.split_cnt;
     STAGE(mfma_ ? launch_gemm_gate_up_mfma(dt_, g1, s) : launch_gemm_gate_up_simt(dt_, g1, s),
           "gate/up GEMM");
     if ((rc = mark(4))) return rc;
 
     GemmArgs g2 = g1;
-    g2.X = d_h_;
+    g2.X = w.h;
     g2.W = d_w2_;
     g2.bias = d_b2_;
-    g2.out = d_yperm_;
+    g2.out = w.yperm;
     g2.N = (int)D_;
     g2.K = (int)H_;
     STAGE(mfma_ ? launch_gemm_down_mfma(dt_, g2, s) : launch_gemm_down_simt(dt_, g2, s),
@@ -494,25 +521,20 @@ int MoeLayer::forward_impl(const void* x, void* y, int64_t rows, hipStream_t s,
     if ((rc = mark(5))) return rc;
 
     CombineArgs ca;
-    ca.y_perm = d_yperm_;
-    ca.tok_pos = d_pos_;
-    ca.topk_w = d_w_;
+    ca.y_perm = w.yperm;
+    ca.tok_pos = w.pos;
+    ca.topk_w = w.w;
     ca.rows = rows;
     ca.D = (int)D_;
     ca.k_slots = (int)kslots_;
     ca.out = y;
-    ca.a_cap = cap_rows_ * kslots_;
+    ca.a_cap = a_cap;
     ca.resid_x = blk ? x : nullptr;
     ca.gate = blk ? blk->gate : nullptr;
     ca.seq = blk ? blk->seq : 1;
     STAGE(launch_combine(dt_, ca, s), "combine");
     if ((rc = mark(6))) return rc;
 #undef STAGE
-    if (!done_) HIP_TRY(hipEventCreateWithFlags(&done_, kDoneFlags));
-    HIP_TRY(hipEventRecord(done_, s));
-    done_recorded_ = true;
-    last_rows_ = rows;
-    last_stream_ = s;
     return NOMAS_OK;
 }
 
@@ -522,6 +544,7 @@ int MoeLayer::forward_impl(const void* x, void* y, int64_t rows, hipStream_t s,
 // (none).
 int MoeLayer::forward_dense(const void* x, void* y, int64_t rows, hipStream_t s) {
     int rc;
+    const Workspace& w = ws_;
     const int mt = max_tiles(rows);
     hipEvent_t* ev = nullptr;
     if (profiling_) {
@@ -540,33 +563,33 @@ int MoeLayer::forward_dense(const void* x, void* y, int64_t rows, hipStream_t s)
     } while (0)
     if ((rc = mark(0))) return rc;
     if ((rc = mark(1))) return rc;
-    STAGE(launch_dense_tiles(rows, BM_, mt, d_tiles_, d_tile_total_, s), "tile table");
+    STAGE(launch_dense_tiles(rows, BM_, mt, w.tiles, w.tile_total, s), "tile table");
     if ((rc = mark(2))) return rc;
     // the MFMA GEMMs read K-blocked rows; the general path reads x in place
-    if (mfma_) STAGE(launch_kblock(dt_, x, d_xperm_, rows, (int)D_, cap_rows_, s), "K-blocked copy");
+    if (mfma_) STAGE(launch_kblock(dt_, x, w.xperm, rows, (int)D_, w.cap_rows, s), "K-blocked copy");
     if ((rc = mark(3))) return rc;
 
     GemmArgs g1;
-    g1.X = mfma_ ? d_xperm_ : x;
+    g1.X = mfma_ ? w.xperm : x;
     g1.W = d_w1_;
     g1.bias = d_b1_;
-    g1.out = d_h_;
-    g1.tiles = d_tiles_;
-    g1.tile_total = d_tile_total_;
+    g1.out = w.h;
+    g1.tiles = w.tiles;
+    g1.tile_total = w.tile_total;
     g1.max_tiles = mt;
     g1.N = (int)(2 * H_);
     g1.K = (int)D_;
     g1.num_experts = 1;
     // MFMA: the K-blocked buffers' row capacity; general: rows of x (row-major)
-    g1.a_cap = mfma_ ? cap_rows_ : rows;
-    g1.split_ws = d_split_ws_;
-    g1.split_cnt = d_split_cnt_;
+    g1.a_cap = mfma_ ? w.cap_rows : rows;
+    g1.split_ws = w.split_ws;
+    g1.split_cnt = w.split_cnt;
     STAGE(mfma_ ? launch_gemm_gate_up_mfma(dt_, g1, s) : launch_gemm_gate_up_simt(dt_, g1, s),
           "gate/up GEMM");
     if ((rc = mark(4))) return rc;
 
     GemmArgs g2 = g1;
-    g2.X = d_h_;
+    g2.X = w.h;
     g2.W = d_w2_;
     g2.bias = d_b2_;
     g2.out = y;  // rows stay in order: the output is y itself
@@ -577,12 +600,8 @@ int MoeLayer::forward_dense(const void* x, void* y, int64_t rows, hipStream_t s)
     if ((rc = mark(5))) return rc;
     if ((rc = mark(6))) return rc;
 #undef STAGE
-    if (!done_) HIP_TRY(hipEventCreateWithFlags(&done_, kDoneFlags));
-    HIP_TRY(hipEventRecord(done_, s));
-    done_recorded_ = true;
-    last_rows_ = rows;
-    last_stream_ = s;
-    return NOMAS_OK;
+    last_in_scratch_ = false;
+    return finish_forward(rows, s, w);
 }
 
 int MoeLayer::forward_host(const void* x, void* y, int64_t rows) {
@@ -623,16 +642,16 @@ int MoeLayer::routing(int32_t* idx, float* w, int32_t* counts, float* gap) {
     if (idx || w) {
         std::vector<int32_t> hi((size_t)(rows * kslots_));
         std::vector<float> hw((size_t)(rows * kslots_));
-        HIP_TRY(hipMemcpy(hi.data(), d_idx_, hi.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
-        HIP_TRY(hipMemcpy(hw.data(), d_w_, hw.size() * sizeof(float), hipMemcpyDeviceToHost));
+        HIP_TRY(hipMemcpy(hi.data(), last_ws_.idx, hi.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
+        HIP_TRY(hipMemcpy(hw.data(), last_ws_.w, hw.size() * sizeof(float), hipMemcpyDeviceToHost));
         for (int64_t r = 0; r < rows; ++r)
             for (int64_t j = 0; j < k_; ++j) {
                 if (idx) idx[r * k_ + j] = hi[(size_t)(r * kslots_ + j)];
                 if (w) w[r * k_ + j] = hw[(size_t)(r * kslots_ + j)];
             }
     }
-    if (counts) HIP_TRY(hipMemcpy(counts, d_expert_count_, sizeof(int32_t) * E_, hipMemcpyDeviceToHost));
-    if (gap) HIP_TRY(hipMemcpy(gap, d_gap_, sizeof(float) * rows, hipMemcpyDeviceToHost));
+    if (counts) HIP_TRY(hipMemcpy(counts, last_ws_.expert_count, sizeof(int32_t) * E_, hipMemcpyDeviceToHost));
+    if (gap) HIP_TRY(hipMemcpy(gap, last_ws_.gap, sizeof(float) * rows, hipMemcpyDeviceToHost));
     return NOMAS_OK;
 }
 
