@@ -292,6 +292,14 @@ int nomas_moe_forward(nomas_moe_t* h, const void* x, void* y, int64_t rows, void
     });
 }
 
+int nomas_moe_forward_noalloc(nomas_moe_t* h, const void* x, void* y, int64_t rows, void* stream) {
+    return guarded(__func__, [&]() -> int {
+        nomas::clear_error();
+        if (!h) return set_error(NOMAS_ERR_INVALID_ARGUMENT, "null handle");
+        return h->layer->forward_noalloc(x, y, rows, static_cast<hipStream_t>(stream));
+    });
+}
+
 int nomas_moe_forward_block(nomas_moe_t* h, const void* x, void* out, int64_t rows, int64_t seq,
                             const float* norm_w, double eps, const float* shift,
                             const float* scale, const float* gate, void* stream) {

@@ -87,10 +87,11 @@ int st_to_f32(const StTensor& t, std::vector<float>* out);
 
 // ---- the layer -----------------------------------------------------------
 
-// Device buffers of one forward, kept by the handle (grown as needed).  The
-// split-tile counters and partials come first, at offsets that do not depend
-// on the row count, so counters left at zero by one forward are where the
-// next one looks for them.
+// Device buffers of one forward.  The handle keeps its own (grown as
+// needed); the no-allocation forward lays the same buffers out in the
+// device's scratch array.  The split-tile counters and partials come first,
+// at offsets that do not depend on the row count, so counters left at zero
+// by one forward are where the next one looks for them.
 struct Workspace {
     int64_t cap_rows = 0;  // rows the buffers are laid out for (a multiple of 64)
     int32_t* split_cnt = nullptr;    // MFMA path: arrival counters of K-split tiles
@@ -110,6 +111,11 @@ struct Workspace {
     void* block_h = nullptr;         // forward_block: rows x D
 };
 
+// The device scratch array of the no-allocation forward (scratch.hip).
+constexpr size_t kScratchBytes = (size_t)256 << 20;
+// Its address on `device` (looked up once per device; the first call also
+// clears the split-tile counters with a kernel on `s`).  Never allocates.
+int scratch_acquire(int device, hipStream_t s, void** out);
 
 // Parameters of one Lin in f32, reference (out, in) layout.
 struct LinF32 {
@@ -150,6 +156,9 @@ public:
     int upload_f32(const MoeParamsF32& p);
 
     int forward(const void* x, void* y, int64_t rows, hipStream_t s);
+    // forward() with every device buffer in the device's scratch array: no
+    // allocation, and an error if `rows` needs more than kScratchBytes.
+    int forward_noalloc(const void* x, void* y, int64_t rows, hipStream_t s);
     // The FFN half of a DiT block around the MoE (block.rs:96-101):
     // out = x + moe(modulate(norm2(x), shift, scale)) * gate, with (rows / seq,
     // D) f32 shift / scale / gate and an optional f32 norm gain, all device

@@ -401,6 +401,41 @@ int MoeLayer::forward_impl(const void* x, void* y, int64_t rows, hipStream_t s,
     return finish_forward(rows, s, ws_);
 }
 
+int MoeLayer::forward_noalloc(const void* x, void* y, int64_t rows, hipStream_t s) {
+    if (dense_only_)
+        return set_error(NOMAS_ERR_STATE, "the no-allocation forward is implemented for the MoE layer");
+    int rc = check_forward(x, y, rows);
+    if (rc != NOMAS_OK) return rc;
+    if (rows == 0) { last_rows_ = 0; last_in_scratch_ = false; return NOMAS_OK; }
+    const int64_t cap = (rows + kRouterRows - 1) / kRouterRows * kRouterRows;
+    const size_t need = layout(cap, false, nullptr, nullptr);
+    if (need > kScratchBytes) {
+        // the most rows that fit, for the message
+        int64_t lo = 0, hi = cap / kRouterRows;
+        while (lo < hi) {
+            const int64_t mid = (lo + hi + 1) / 2;
+            if (layout(mid * kRouterRows, false, nullptr, nullptr) <= kScratchBytes) lo = mid;
+            else hi = mid - 1;
+        }
+        return set_error(NOMAS_ERR_INVALID_ARGUMENT,
+                         "rows=%lld need %zu bytes of device scratch; the no-allocation forward "
+                         "holds %zu (at most %lld rows for this layer): use nomas_moe_forward",
+                         (long long)rows, need, kScratchBytes, (long long)(lo * kRouterRows));
+    }
+    DeviceGuard g(device_);
+    if (!g.ok) return set_error(NOMAS_ERR_HIP, "hipSetDevice(%d) failed", device_);
+    void* base = nullptr;
+    rc = scratch_acquire(device_, s, &base);
+    if (rc != NOMAS_OK) return rc;
+    Workspace w;
+    layout(cap, false, static_cast<uint8_t*>(base), &w);
+    if (done_recorded_ && s != last_stream_) HIP_TRY(hipStreamWaitEvent(s, done_, 0));
+    rc = run_routed(x, y, rows, s, nullptr, w);
+    if (rc != NOMAS_OK) return rc;
+    last_in_scratch_ = true;
+    return finish_forward(rows, s, w);
+}
+
 int MoeLayer::finish_forward(int64_t rows, hipStream_t s, const Workspace& w) {
     // done_ is created with the weights; recording it allocates nothing
     HIP_TRY(hipEventRecord(done_, s));

@@ -51,6 +51,8 @@ def lib() -> C.CDLL:
     L.nomas_moe_from_host.restype = i32
     L.nomas_moe_forward.argtypes = [vp, vp, vp, i64, vp]
     L.nomas_moe_forward.restype = i32
+    L.nomas_moe_forward_noalloc.argtypes = [vp, vp, vp, i64, vp]
+    L.nomas_moe_forward_noalloc.restype = i32
     L.nomas_moe_forward_block.argtypes = [vp, vp, vp, i64, i64, vp, C.c_double, vp, vp, vp, vp]
     L.nomas_moe_forward_block.restype = i32
     L.nomas_moe_forward_host.argtypes = [vp, vp, vp, i64]

@@ -100,6 +100,21 @@ int nomas_moe_from_host(const nomas_moe_config *cfg, int64_t dim, int64_t hidden
  * hipStream_t (NULL = default stream).  Asynchronous with respect to the host. */
 int nomas_moe_forward(nomas_moe_t *h, const void *x, void *y, int64_t rows, void *stream);
 
+/* No counterpart in the reference: nomas_moe_forward for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments and results, but every device buffer of
+ * the forward (routing, permuted rows, the SwiGLU intermediate, K-split
+ * partials) lives in a static device array of 256 MiB per GPU, held until
+ * the process ends: the call allocates nothing.  `rows` beyond what fits (it
+ * depends on dim, hidden and top_k; 3,456 rows at dim 3072, hidden 8192,
+ * top-2) is NOMAS_ERR_INVALID_ARGUMENT with the limit in the message.  The
+ * first call on a device looks up the array's address and clears its
+ * counters with a kernel on `stream`.  All such calls on one GPU share the
+ * array: calls that overlap on one GPU (different streams, threads or
+ * handles) race, and routing() after such a call reads the array, valid
+ * until the next one. */
+int nomas_moe_forward_noalloc(nomas_moe_t *h, const void *x, void *y, int64_t rows, void *stream);
+
 /* The FFN half of DiTBlock::forward around the MoE (block.rs:96-101), fused
  * into the MoE's own kernels:
  *   h   = modulate(norm2(x), shift, scale)     (norm.rs:55-65, modulate.rs:69-79)
