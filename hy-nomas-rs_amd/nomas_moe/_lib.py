@@ -13,7 +13,9 @@ import os
 import torch  # noqa: F401  (must be loaded before the library, see above)
 
 _PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(_PKG_ROOT, "libnomas_moe.so")
+# NOMAS_MOE_LIB selects another build of the same library (the sanitizer
+# build, libnomas_moe_san.so, in the CPU tests)
+LIB_PATH = os.environ.get("NOMAS_MOE_LIB") or os.path.join(_PKG_ROOT, "libnomas_moe.so")
 
 _lib = None
 

@@ -17,7 +17,8 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+# NOMAS_ORACLE_LIB selects another build (the sanitizer build, liboracle_san.so)
+_LIB_PATH = os.environ.get("NOMAS_ORACLE_LIB") or os.path.join(_HERE, "liboracle.so")
 _lib = None
 
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
