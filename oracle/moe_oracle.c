@@ -59,7 +59,13 @@ enum {
     MUT_MODULATE_NO_ONE = 9,  /* modulate multiplies by scale, not 1 + scale    */
     MUT_VAR_D_MINUS_1 = 10,   /* RMSNorm mean over D - 1 elements               */
     MUT_NORM_NO_ROUND = 11,   /* norm output not rounded to the model dtype     */
-    MUT_UNGATED_RESIDUAL = 12 /* residual adds y without the gate               */
+    MUT_UNGATED_RESIDUAL = 12, /* residual adds y without the gate              */
+    MUT_H_UNROUNDED = 13,     /* rounded mode: SwiGLU intermediate kept in f64  */
+    MUT_COMBINE_UNFUSED = 14, /* rounded mode: combine as f32 mul, then add     */
+    /* a simulated GPU-path fault (tests/test_parity_bars.py), not an oracle
+     * mistake: the gate/up GEMM skips x[32..39] for hidden units 0..15, one
+     * 16-byte operand fragment of one k step of one 16-row MFMA block */
+    MUT_GATE_UP_LOSES_FRAGMENT = 15
 };
 
 /* ------------------------------------------------------------------ */
@@ -243,20 +249,33 @@ void orc_route_f64(int64_t T, int64_t D, int64_t E, int64_t k, const float *x, c
 
 static double silu(double g) { return g / (1.0 + exp(-g)); }
 
-/* One SwiGLU FFN (mlp.rs:42-46) on one row, f64: y = down(silu(gate x) * up x). */
+static float round_dt(float v, int dt);
+
+/* The kernels' storage of an intermediate in the model dtype: the f64 value
+ * rounded to f32 (their accumulators), then to the model dtype; rdt < 0
+ * keeps the f64 value. */
+static double stored(double v, int rdt)
+{
+    return rdt < 0 ? v : (double)round_dt((float)v, rdt);
+}
+
+/* One SwiGLU FFN (mlp.rs:42-46) on one row, f64: y = down(silu(gate x) * up x).
+ * rdt >= 0 stores the SwiGLU intermediate a and the output y in the model
+ * dtype rdt, as the GPU path's buffers hold them (see stored()). */
 static void swiglu_row_f64(int64_t D, int64_t H, const float *x, const float *wg, const float *bg,
                            const float *wu, const float *bu, const float *wd, const float *bd,
-                           double *a, double *y)
+                           double *a, double *y, int rdt)
 {
     for (int64_t h = 0; h < H; ++h) {
         double g = bg ? (double)bg[h] : 0.0, u = bu ? (double)bu[h] : 0.0;
         const float *gr = wg + h * D, *ur = wu + h * D;
         for (int64_t d = 0; d < D; ++d) {
+            if (orc_mutation == MUT_GATE_UP_LOSES_FRAGMENT && h < 16 && d >= 32 && d < 40) continue;
             g += (double)x[d] * (double)gr[d];
             u += (double)x[d] * (double)ur[d];
         }
         if (orc_mutation == MUT_SWAP_GATE_UP) { double t = g; g = u; u = t; }
-        a[h] = silu(g) * u;
+        a[h] = orc_mutation == MUT_H_UNROUNDED ? silu(g) * u : stored(silu(g) * u, rdt);
     }
     for (int64_t d = 0; d < D; ++d) {
         double s = (bd && orc_mutation != MUT_DROP_DOWN_BIAS) ? (double)bd[d] : 0.0;
@@ -269,7 +288,7 @@ static void swiglu_row_f64(int64_t D, int64_t H, const float *x, const float *wg
             for (int64_t h = 0; h < H; ++h)
                 s += a[h] * (double)dr[h];
         }
-        y[d] = s;
+        y[d] = stored(s, rdt);
     }
 }
 
@@ -285,7 +304,7 @@ void orc_ffn_f64(int64_t D, int64_t H, const float *x, const float *wg, const fl
 #pragma omp for schedule(dynamic, 1)
         for (int64_t r = 0; r < nrows; ++r) {
             int64_t t = rows ? rows[r] : r;
-            swiglu_row_f64(D, H, x + t * D, wg, bg, wu, bu, wd, bd, a, out + r * D);
+            swiglu_row_f64(D, H, x + t * D, wg, bg, wu, bu, wd, bd, a, out + r * D, -1);
         }
         free(a);
     }
@@ -296,14 +315,14 @@ void orc_ffn_f64(int64_t D, int64_t H, const float *x, const float *wg, const fl
  * (dense_* pointers, coefficient s) is added after the experts when s > 0,
  * additively as moe.rs:103-106 does.  Also writes each row's routing when
  * idx/w/gap are non-NULL (k entries per row, ascending expert index). */
-void orc_forward_sparse_f64(int64_t D, int64_t E, int64_t k, int64_t H,
-                            const float *x, const float *wr,
-                            const float *wg, const float *bg, const float *wu, const float *bu,
-                            const float *wd, const float *bd,
-                            double s, const float *dwg, const float *dbg, const float *dwu,
-                            const float *dbu, const float *dwd, const float *dbd,
-                            const int64_t *rows, int64_t nrows, double *out,
-                            int32_t *idx_out, double *w_out, double *gap_out)
+static void forward_sparse(int64_t D, int64_t E, int64_t k, int64_t H,
+                           const float *x, const float *wr,
+                           const float *wg, const float *bg, const float *wu, const float *bu,
+                           const float *wd, const float *bd,
+                           double s, const float *dwg, const float *dbg, const float *dwu,
+                           const float *dbu, const float *dwd, const float *dbd,
+                           const int64_t *rows, int64_t nrows, double *out,
+                           int32_t *idx_out, double *w_out, double *gap_out, int rdt)
 {
 #pragma omp parallel
     {
@@ -317,18 +336,37 @@ void orc_forward_sparse_f64(int64_t D, int64_t E, int64_t k, int64_t H,
             route_row_f64(D, E, k, xr, wr, li, lw, lg, &g, scr);
             double *o = out + r * D;
             for (int64_t d = 0; d < D; ++d) o[d] = 0.0;
+            /* rdt >= 0: the GPU combine -- per element, an f32 fused
+             * multiply-add of the stored y by the f32 gate, slot by slot in
+             * ascending expert order (then the dense slot), the sum rounded
+             * once to the model dtype */
             for (int64_t j = 0; j < k; ++j) {
                 int64_t e = li[j];
                 if (e < 0) continue;
                 swiglu_row_f64(D, H, xr, wg + e * H * D, bg ? bg + e * H : NULL,
                                wu + e * H * D, bu ? bu + e * H : NULL,
-                               wd + e * D * H, bd ? bd + e * D : NULL, a, y);
-                for (int64_t d = 0; d < D; ++d) o[d] += lw[j] * y[d];
+                               wd + e * D * H, bd ? bd + e * D : NULL, a, y, rdt);
+                if (rdt < 0)
+                    for (int64_t d = 0; d < D; ++d) o[d] += lw[j] * y[d];
+                else if (orc_mutation == MUT_COMBINE_UNFUSED)
+                    for (int64_t d = 0; d < D; ++d) {
+                        const float m = (float)y[d] * (float)lw[j];
+                        o[d] = (double)((float)o[d] + m);
+                    }
+                else
+                    for (int64_t d = 0; d < D; ++d)
+                        o[d] = (double)fmaf((float)y[d], (float)lw[j], (float)o[d]);
             }
             if (s > 0.0 && dwg) {
-                swiglu_row_f64(D, H, xr, dwg, dbg, dwu, dbu, dwd, dbd, a, y);
-                for (int64_t d = 0; d < D; ++d) o[d] += s * y[d];
+                swiglu_row_f64(D, H, xr, dwg, dbg, dwu, dbu, dwd, dbd, a, y, rdt);
+                if (rdt < 0)
+                    for (int64_t d = 0; d < D; ++d) o[d] += s * y[d];
+                else
+                    for (int64_t d = 0; d < D; ++d)
+                        o[d] = (double)fmaf((float)y[d], (float)s, (float)o[d]);
             }
+            if (rdt >= 0)
+                for (int64_t d = 0; d < D; ++d) o[d] = (double)round_dt((float)o[d], rdt);
             if (idx_out) memcpy(idx_out + r * k, li, sizeof(int32_t) * (size_t)k);
             if (w_out) memcpy(w_out + r * k, lw, sizeof(double) * (size_t)k);
             if (gap_out) gap_out[r] = g;
@@ -336,6 +374,38 @@ void orc_forward_sparse_f64(int64_t D, int64_t E, int64_t k, int64_t H,
         free(scr);
         free(li);
     }
+}
+
+void orc_forward_sparse_f64(int64_t D, int64_t E, int64_t k, int64_t H,
+                            const float *x, const float *wr,
+                            const float *wg, const float *bg, const float *wu, const float *bu,
+                            const float *wd, const float *bd,
+                            double s, const float *dwg, const float *dbg, const float *dwu,
+                            const float *dbu, const float *dwd, const float *dbd,
+                            const int64_t *rows, int64_t nrows, double *out,
+                            int32_t *idx_out, double *w_out, double *gap_out)
+{
+    forward_sparse(D, E, k, H, x, wr, wg, bg, wu, bu, wd, bd, s, dwg, dbg, dwu, dbu, dwd, dbd,
+                   rows, nrows, out, idx_out, w_out, gap_out, -1);
+}
+
+/* The same forward with the GPU path's storage roundings: the SwiGLU
+ * intermediate and each expert's output held in the model dtype dt (0 f32,
+ * 1 bf16, 2 f16), the combine an f32 fused multiply-add per slot, the output
+ * rounded to dt.  Not the reference's arithmetic (candle rounds after every
+ * op): it isolates the kernels' own error from the storage roundings, so a
+ * tight bar against it catches mistakes (a lost k step, a stale partial)
+ * that the loose bar against the f64 forward would let through. */
+void orc_forward_sparse_rounded(int64_t D, int64_t E, int64_t k, int64_t H,
+                                const float *x, const float *wr,
+                                const float *wg, const float *bg, const float *wu, const float *bu,
+                                const float *wd, const float *bd,
+                                double s, const float *dwg, const float *dbg, const float *dwu,
+                                const float *dbu, const float *dwd, const float *dbd,
+                                const int64_t *rows, int64_t nrows, double *out, int dt)
+{
+    forward_sparse(D, E, k, H, x, wr, wg, bg, wu, bu, wd, bd, s, dwg, dbg, dwu, dbu, dwd, dbd,
+                   rows, nrows, out, NULL, NULL, NULL, dt < 0 ? 0 : dt);
 }
 
 /* ------------------------------------------------------------------ */

@@ -58,6 +58,10 @@ def lib():
     L.orc_forward_sparse_f64.argtypes = (
         [C.c_int64] * 4 + [C.c_void_p] * 8 + [C.c_double] + [C.c_void_p] * 6
         + [C.c_void_p, C.c_int64, _f64p, C.c_void_p, C.c_void_p, C.c_void_p])
+    L.orc_forward_sparse_rounded.restype = None
+    L.orc_forward_sparse_rounded.argtypes = (
+        [C.c_int64] * 4 + [C.c_void_p] * 8 + [C.c_double] + [C.c_void_p] * 6
+        + [C.c_void_p, C.c_int64, _f64p, C.c_int])
     L.orc_ffn_f64.restype = None
     L.orc_ffn_f64.argtypes = [C.c_int64] * 2 + [C.c_void_p] * 7 + [C.c_void_p, C.c_int64, _f64p]
     L.orc_forward_dense_f32.restype = C.c_int
@@ -95,6 +99,15 @@ MUTATIONS = {
     "var_d_minus_1": 10,
     "norm_no_round": 11,
     "ungated_residual": 12,
+    "h_unrounded": 13,
+    "combine_unfused": 14,
+}
+
+# Faults of the GPU path simulated in the oracle (not oracle mistakes): the
+# parity tests offer their output as if it were the GPU's, to show which bar
+# rejects it.
+KERNEL_FAULTS = {
+    "gate_up_loses_fragment": 15,
 }
 
 
@@ -229,6 +242,29 @@ def forward_sparse(x, p, k, rows=None, shared_dense=0.0, dense=None):
                                  float(shared_dense), *[_ptr(a) for a in dn],
                                  _ptr(rows_a), n, out, _ptr(idx), _ptr(w), _ptr(gap))
     return out, idx, w, gap
+
+
+def forward_sparse_rounded(x, p, k, dt, rows=None, shared_dense=0.0, dense=None):
+    """forward_sparse with the GPU path's storage roundings (dt "f32" / "bf16" /
+    "f16"): the SwiGLU intermediate and each expert's output held in the model
+    dtype, the combine an f32 fused multiply-add per slot in ascending expert
+    order, the output rounded to dt.  Returns out[n,D] f64 (values of dt)."""
+    x = _f32(x)
+    T, D = x.shape
+    E, H = p["wg"].shape[0], p["wg"].shape[1]
+    arrs = [_f32(p.get(n)) for n in ("wr", "wg", "bg", "wu", "bu", "wd", "bd")]
+    dn = [None] * 6 if dense is None else [_f32(dense.get(n)) for n in
+                                           ("wg", "bg", "wu", "bu", "wd", "bd")]
+    if rows is None:
+        rows_a, n = None, T
+    else:
+        rows_a = np.ascontiguousarray(rows, dtype=np.int64)
+        n = rows_a.size
+    out = np.empty((n, D), np.float64)
+    lib().orc_forward_sparse_rounded(D, E, k, H, _ptr(x), *[_ptr(a) for a in arrs],
+                                     float(shared_dense), *[_ptr(a) for a in dn],
+                                     _ptr(rows_a), n, out, DT_CODE[dt])
+    return out
 
 
 def ffn(x, f, rows=None):

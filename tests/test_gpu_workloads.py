@@ -1,10 +1,15 @@
 """The benchmark workloads at full size on the GPU.
 
 Routing (expert indices and per-expert counts) is checked on every row
-against the oracle's f64 routing; outputs on a seeded sample of rows (the
-oracle's sparse f64 forward is exact per row, rows are independent), plus
-size-independent properties: counts sum to rows * k, every row finite, and a
-second forward is bitwise identical.
+against the oracle's f64 routing.  Outputs are checked on rows chosen by
+construction so that every (expert, 256-row tile) of the grouped GEMMs is
+covered at six offsets (both wave halves, several 16-row MFMA blocks, the
+last live row of short tail tiles); a checked row covers every column tile
+of its row tiles, including tiles split along K (rows are independent, so
+the oracle evaluates exactly those rows).  Two bars
+against the f64 oracle, and a tight bar against the oracle with the GPU
+path's storage roundings.  Size-independent properties: counts sum to
+rows * k, every row finite, a second forward bitwise identical.
 """
 import numpy as np
 import pytest
@@ -13,7 +18,7 @@ import torch
 import nomas_moe as nm
 from nomas_moe import workloads as wl
 import oracle as O
-from _gpu import check_routing, rel_err, to_device, TOL
+from _gpu import TOL, check_routing, check_tight, rel_err, tile_rows, to_device
 
 pytestmark = pytest.mark.gpu
 
@@ -45,13 +50,16 @@ def test_workload(name):
     del rt
     o_idx, o_w, _, o_gap = O.route(rx, p["wr"], w.top_k)
     near = check_routing(layer, w.rows, o_idx, o_w, o_gap, w.experts)
-    _, _, counts, _ = layer.routing(w.rows)
+    g_idx, _, counts, _ = layer.routing(w.rows)
     assert counts.sum() == w.rows * w.top_k
     print(f"  counts {counts.tolist()}  near ties {int(near.sum())}", flush=True)
-    rng = np.random.default_rng(w.base_seed)
-    sample = np.unique(np.concatenate([[0, w.rows - 1], rng.choice(w.rows, 46, replace=False)]))
-    sample = sample[~near[sample]]
-    ref, _, _, _ = O.forward_sparse(rx, p, w.top_k, rows=sample)
-    err = rel_err(got[sample], ref)
-    print(f"  rel err {err:.3e} on {sample.size} sampled rows", flush=True)
+    rows, ntiles = tile_rows(g_idx, w.experts)
+    rows = rows[~near[rows]]
+    tight = check_tight(got[rows], rx, p, w.top_k, dt, rows)
+    print(f"  {rows.size} rows covering {ntiles} expert tiles: vs rounded oracle "
+          f"max {tight[0]:.3e} worst row rms {tight[1]:.3e}", flush=True)
+    sub = rows[::4]  # the f64 forward on every fourth of them
+    ref, _, _, _ = O.forward_sparse(rx, p, w.top_k, rows=sub)
+    err = rel_err(got[sub], ref)
+    print(f"  rel err vs f64 oracle {err:.3e} on {sub.size} rows", flush=True)
     assert err <= TOL[dt]

@@ -211,6 +211,54 @@ def pin_forward_bruteforce():
         np.testing.assert_allclose(got, want, rtol=1e-10, atol=1e-12)
 
 
+def _fmaf(a, b, c):
+    """f32 fused multiply-add: a*b + c with one rounding (the f32 product is
+    exact in x86 long double, and the sum is rounded to 64 bits first, which
+    changes the f32 result only on an exact double-rounding midpoint)."""
+    ld = np.longdouble
+    return (np.asarray(a, ld) * np.asarray(b, ld) + np.asarray(c, ld)).astype(np.float32)
+
+
+def _rounded_moe(x, p, k, dt):
+    """The GPU path's storage roundings, from numpy f64 GEMMs: h and y stored in
+    dt (via f32), the combine an f32 FMA per slot in ascending expert order,
+    the output rounded to dt."""
+    tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[dt]
+
+    def st(v):
+        return torch.from_numpy(np.asarray(v, np.float64).astype(np.float32)).to(tdt).float().numpy()
+
+    idx, w, _ = _np_route(x, p["wr"], k)
+    x64 = x.astype(np.float64)
+    out = np.zeros(x.shape, np.float32)
+    for r in range(x.shape[0]):
+        acc = np.zeros(x.shape[1], np.float32)
+        for j in range(k):
+            e = idx[r, j]
+            g = p["wg"][e].astype(np.float64) @ x64[r] + p["bg"][e]
+            u = p["wu"][e].astype(np.float64) @ x64[r] + p["bu"][e]
+            a = st(g / (1.0 + np.exp(-g)) * u)
+            y = st(p["wd"][e].astype(np.float64) @ a.astype(np.float64) + p["bd"][e])
+            acc = _fmaf(y, np.float32(w[r, j]), acc)
+        out[r] = st(acc)
+    return out
+
+
+def pin_forward_rounded_bruteforce():
+    # orc_forward_sparse_rounded: the same roundings, written independently
+    for (T, D, E, k, H) in [(24, 20, 5, 2, 28), (10, 16, 4, 3, 12)]:
+        p = _params(13, E, D, H)
+        x = np.random.default_rng(14).standard_normal((T, D)).astype(np.float32)
+        for dt in ("f32", "bf16", "f16"):
+            got = O.forward_sparse_rounded(x, p, k, dt)
+            np.testing.assert_array_equal(got.astype(np.float32), _rounded_moe(x, p, k, dt))
+            assert np.array_equal(got, O.round_dt(got.astype(np.float32), dt))
+        # with f32 storage it is the f64 forward to within f32 rounding
+        ref, _, _, _ = O.forward_sparse(x, p, k)
+        f32 = O.forward_sparse_rounded(x, p, k, "f32")
+        assert np.max(np.abs(f32 - ref)) <= 1e-6 * np.max(np.abs(ref))
+
+
 def pin_dense_equals_sparse():
     # the reference's dense evaluation (moe.rs:97-102) equals the sparse one
     p = _params(13, 6, 32, 48)
@@ -422,6 +470,7 @@ PINS = [pin_splitmix64, pin_fnv1a, pin_box_muller, pin_affine_and_moments, pin_u
         pin_xavier_std,
         pin_bf16_rounding, pin_route_bruteforce, pin_route_ties_lowest_index,
         pin_route_one_hot_rows, pin_route_weights_sum_to_one, pin_forward_bruteforce,
+        pin_forward_rounded_bruteforce,
         pin_dense_equals_sparse, pin_k_equals_experts, pin_single_dominant_expert,
         pin_zero_input_zero_output, pin_row_permutation, pin_shared_dense_branch,
         pin_ffn_bruteforce, pin_ffn_equals_single_expert,
