@@ -89,22 +89,27 @@ def make_x(w: Workload, rows: int | None = None) -> np.ndarray:
     return x
 
 
+def make_router(w: Workload) -> np.ndarray:
+    """The router weight (E, D) in f32 (key {path}.router.weight)."""
+    D, E, s = w.dim, w.experts, w.base_seed
+    p = moe_path()
+    if w.router == "normal":
+        return randn_affine(path_seed(s, p + ".router"), E * D, 0.0, 0.02).reshape(E, D)
+    wr = np.empty((E, D), np.float32)
+    wr[:, 1:] = randn_affine(path_seed(s, p + ".router"), E * (D - 1), 0.0,
+                             1.0 / math.sqrt(D - 1)).reshape(E, D - 1)
+    if w.router == "fine64":
+        wr[:, 0] = randn_affine(path_seed(s, p + ".router.logit_bias"), E, 0.0, 0.5)
+    else:
+        wr[:, 0] = np.asarray(SKEW_BIASES[:E], np.float32)
+    return wr
+
+
 def make_params(w: Workload, bias: bool = False, dense: bool = False) -> dict:
     """f32 parameters keyed like the checkpoint (weights.rs:78-93)."""
     D, H, E, s = w.dim, w.hidden, w.experts, w.base_seed
     p = moe_path()
-    t = {}
-    if w.router == "normal":
-        wr = randn_affine(path_seed(s, p + ".router"), E * D, 0.0, 0.02).reshape(E, D)
-    else:
-        wr = np.empty((E, D), np.float32)
-        wr[:, 1:] = randn_affine(path_seed(s, p + ".router"), E * (D - 1), 0.0,
-                                 1.0 / math.sqrt(D - 1)).reshape(E, D - 1)
-        if w.router == "fine64":
-            wr[:, 0] = randn_affine(path_seed(s, p + ".router.logit_bias"), E, 0.0, 0.5)
-        else:
-            wr[:, 0] = np.asarray(SKEW_BIASES[:E], np.float32)
-    t[p + ".router.weight"] = wr
+    t = {p + ".router.weight": make_router(w)}
 
     def lin(path, out_f, in_f, std):
         t[path + ".weight"] = randn_affine(path_seed(s, path), out_f * in_f, 0.0,

@@ -408,6 +408,77 @@ void orc_forward_sparse_rounded(int64_t D, int64_t E, int64_t k, int64_t H,
                    rows, nrows, out, NULL, NULL, NULL, dt < 0 ? 0 : dt);
 }
 
+/* Routing of a model in dtype dt (0 f32, 1 bf16, 2 f16) as the reference
+ * evaluates it, op by op in the tensor dtype (moe.rs:67-95): PARITY UNPINNED.
+ * candle cannot be built or imported here, so its per-op semantics are
+ * restated from its documented behaviour and not checked against it:
+ *   logits = x . wr^T accumulated in f32, rounded to dt (candle's CPU matmul
+ *            of half types accumulates in f32);
+ *   softmax composed (candle_nn::ops::softmax): m = max; diff = dt(l - m);
+ *            num = dt(exp(diff)); den = the num summed one add at a time in
+ *            dt, ascending expert; p = dt(num / den);
+ *   top-k:   k passes of argmax over the remaining p (first maximum wins),
+ *            each pass zeroing the chosen entry (moe.rs:77-91);
+ *   gates:   norm = the chosen p summed in dt; w = dt(p / dt(norm + dt(1e-9)))
+ *            (moe.rs:92-95).
+ * Used to measure how often a model-dtype router would choose another expert
+ * set than the f64 routing the GPU path follows.  idx (T x k, ascending), w
+ * (T x k) may be NULL. */
+void orc_route_model_dtype(int64_t T, int64_t D, int64_t E, int64_t k, const float *x,
+                           const float *wr, int dt, int32_t *idx, float *w)
+{
+#pragma omp parallel
+    {
+        float *p = (float *)malloc(sizeof(float) * (size_t)(3 * E));
+        float *rem = p + E, *top = p + 2 * E;
+#pragma omp for schedule(static)
+        for (int64_t t = 0; t < T; ++t) {
+            const float *xr = x + t * D;
+            for (int64_t e = 0; e < E; ++e) {
+                float s = 0.0f;
+                const float *we = wr + e * D;
+                for (int64_t d = 0; d < D; ++d) s += xr[d] * we[d];
+                p[e] = round_dt(s, dt);
+            }
+            float m = p[0];
+            for (int64_t e = 1; e < E; ++e) if (p[e] > m) m = p[e];
+            float den = 0.0f;
+            for (int64_t e = 0; e < E; ++e) {
+                p[e] = round_dt(expf(round_dt(p[e] - m, dt)), dt);
+                den = round_dt(den + p[e], dt);
+            }
+            for (int64_t e = 0; e < E; ++e) {
+                rem[e] = round_dt(p[e] / den, dt);
+                top[e] = 0.0f;
+            }
+            for (int64_t it = 0; it < k; ++it) {
+                int64_t best = 0;
+                for (int64_t e = 1; e < E; ++e) if (rem[e] > rem[best]) best = e;
+                top[best] = rem[best];
+                rem[best] = 0.0f;
+            }
+            float norm = 0.0f;
+            for (int64_t e = 0; e < E; ++e) norm = round_dt(norm + top[e], dt);
+            const float dnorm = round_dt(norm + round_dt(1e-9f, dt), dt);
+            int64_t j = 0;
+            for (int64_t e = 0; e < E && j < k; ++e) {
+                /* chosen entries: zeroed in rem; a chosen p of 0 (underflow) is
+                 * listed too, by the order of the passes */
+                if (rem[e] == 0.0f && (top[e] > 0.0f || p[e] == 0.0f)) {
+                    if (idx) idx[t * k + j] = (int32_t)e;
+                    if (w) w[t * k + j] = round_dt(top[e] / dnorm, dt);
+                    ++j;
+                }
+            }
+            for (; j < k; ++j) {
+                if (idx) idx[t * k + j] = -1;
+                if (w) w[t * k + j] = 0.0f;
+            }
+        }
+        free(p);
+    }
+}
+
 /* ------------------------------------------------------------------ */
 /* Faithful dense f32 forward (the reference algorithm; CPU baseline)   */
 /* ------------------------------------------------------------------ */

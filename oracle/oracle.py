@@ -62,6 +62,9 @@ def lib():
     L.orc_forward_sparse_rounded.argtypes = (
         [C.c_int64] * 4 + [C.c_void_p] * 8 + [C.c_double] + [C.c_void_p] * 6
         + [C.c_void_p, C.c_int64, _f64p, C.c_int])
+    L.orc_route_model_dtype.restype = None
+    L.orc_route_model_dtype.argtypes = [C.c_int64] * 4 + [_f32p, _f32p, C.c_int, C.c_void_p,
+                                                          C.c_void_p]
     L.orc_ffn_f64.restype = None
     L.orc_ffn_f64.argtypes = [C.c_int64] * 2 + [C.c_void_p] * 7 + [C.c_void_p, C.c_int64, _f64p]
     L.orc_forward_dense_f32.restype = C.c_int
@@ -213,6 +216,19 @@ def route(x, wr, k):
     gap = np.empty(T, np.float64)
     lib().orc_route_f64(T, D, E, k, x, wr, _ptr(idx), _ptr(w), _ptr(logits), _ptr(gap))
     return idx, w, logits, gap
+
+
+def route_model_dtype(x, wr, k, dt):
+    """Routing op by op in the model dtype as candle evaluates moe.rs:67-95
+    (PARITY UNPINNED: a restatement of candle's per-op rounding that no
+    reference output checks).  x, wr hold values of dt.  Returns (idx[T,k]
+    ascending, w[T,k] f32)."""
+    x, wr = _f32(x), _f32(wr)
+    T, D = x.shape
+    idx = np.empty((T, k), np.int32)
+    w = np.empty((T, k), np.float32)
+    lib().orc_route_model_dtype(T, D, wr.shape[0], k, x, wr, DT_CODE[dt], _ptr(idx), _ptr(w))
+    return idx, w
 
 
 def forward_sparse(x, p, k, rows=None, shared_dense=0.0, dense=None):

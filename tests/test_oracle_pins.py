@@ -259,6 +259,28 @@ def pin_forward_rounded_bruteforce():
         assert np.max(np.abs(f32 - ref)) <= 1e-6 * np.max(np.abs(ref))
 
 
+def pin_route_model_dtype_structure():
+    # orc_route_model_dtype: its candle-specific rounding is unpinned, but its
+    # structure is not: in f32 it chooses the f64 routing's experts (the
+    # random logits here have no near ties), exact ties go to the lowest
+    # index, and the gates sum to one in the model dtype
+    rng = np.random.default_rng(21)
+    for (T, D, E, k) in [(300, 64, 8, 2), (200, 48, 16, 5)]:
+        x = rng.standard_normal((T, D)).astype(np.float32)
+        wr = (rng.standard_normal((E, D)) * 0.3).astype(np.float32)
+        i64, _, _, gap = O.route(x, wr, k)
+        i32, w32 = O.route_model_dtype(x, wr, k, "f32")
+        ok = gap > 1e-4
+        np.testing.assert_array_equal(i32[ok], i64[ok])
+        np.testing.assert_allclose(w32.sum(axis=1), 1.0, atol=1e-5)
+        xb, wb = O.round_bf16(x), O.round_bf16(wr)
+        wb[3] = wb[1]  # experts 1 and 3 always tie exactly
+        ib, gb = O.route_model_dtype(xb, wb, k, "bf16")
+        assert not ((ib == 3).any(axis=1) & ~(ib == 1).any(axis=1)).any()
+        assert np.array_equal(gb, O.round_bf16(gb))
+        np.testing.assert_allclose(gb.astype(np.float64).sum(axis=1), 1.0, atol=2e-2)
+
+
 def pin_dense_equals_sparse():
     # the reference's dense evaluation (moe.rs:97-102) equals the sparse one
     p = _params(13, 6, 32, 48)
@@ -470,7 +492,7 @@ PINS = [pin_splitmix64, pin_fnv1a, pin_box_muller, pin_affine_and_moments, pin_u
         pin_xavier_std,
         pin_bf16_rounding, pin_route_bruteforce, pin_route_ties_lowest_index,
         pin_route_one_hot_rows, pin_route_weights_sum_to_one, pin_forward_bruteforce,
-        pin_forward_rounded_bruteforce,
+        pin_forward_rounded_bruteforce, pin_route_model_dtype_structure,
         pin_dense_equals_sparse, pin_k_equals_experts, pin_single_dominant_expert,
         pin_zero_input_zero_output, pin_row_permutation, pin_shared_dense_branch,
         pin_ffn_bruteforce, pin_ffn_equals_single_expert,
