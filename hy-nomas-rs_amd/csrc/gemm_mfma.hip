@@ -38,6 +38,7 @@
 #include <type_traits>
 
 #include "kernels.hpp"
+#include "lds_dma.hpp"
 #include "tile_map.hpp"
 
 namespace nomas {
@@ -85,35 +86,9 @@ constexpr int kStages = 4;  // LDS ring depth; the main loop is unrolled over on
 // 8 distinct (row parity, chunk) bank groups.
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & 3; }
 
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// Direct global->LDS load of 16 bytes per lane from sbase + voff (a uniform
-// 64-bit base in SGPRs plus a per-lane 32-bit byte offset): lane l's bytes
-// land at LDS address lds_base + 16 * l (global_load_lds_dwordx4, M0 = LDS
-// base; one wait state between the M0 write and the load).  Issued as inline
-// assembly so the compiler does not track it: completion is waited for
-// explicitly with wait_vmcnt, and nothing else in these kernels uses M0.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"  // M0 is clobbered on purpose, see above
-__device__ __forceinline__ void lds_dma16(const void* sbase, uint32_t voff, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-                 :
-                 : "v"(voff), "s"(sbase), "s"(lds_base)
-                 : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
 // Word 3 of a raw buffer resource (gfx9 family: 32-bit data format, no
 // swizzle); with stride 0 the buffer is a plain byte range [0, num_records).
 constexpr int kBufferRsrcWord3 = 0x00020000;
-
-template <typename P>
-__device__ __forceinline__ uint32_t lds_addr(P* p) {
-    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
-}
 
 template <typename T, int MODE, int BM, int BN, int BK, int S>
 __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {

@@ -1,0 +1,37 @@
+// Direct global->LDS loads and the waits that go with them (device code).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nomas {
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Direct global->LDS load of 16 bytes per lane from sbase + voff (a uniform
+// 64-bit base in SGPRs plus a per-lane 32-bit byte offset): lane l's bytes
+// land at LDS address lds_base + 16 * l (global_load_lds_dwordx4, M0 = LDS
+// base; one wait state between the M0 write and the load).  Issued as inline
+// assembly so the compiler does not track it: completion is waited for
+// explicitly with wait_vmcnt, and nothing else in the kernels that use it
+// touches M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // M0 is clobbered on purpose, see above
+__device__ __forceinline__ void lds_dma16(const void* sbase, uint32_t voff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff), "s"(sbase), "s"(lds_base)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// The LDS byte address of a __shared__ object (for M0).
+template <typename P>
+__device__ __forceinline__ uint32_t lds_addr(P* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+}  // namespace nomas

@@ -32,7 +32,9 @@
 //    gate `dense_coef` (moe.rs:103-106 adds it after the experts).
 //  The kernel reads x once (T*D*b bytes) and the router weights from L2.
 #include "kernels.hpp"
+#include "lds_dma.hpp"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace nomas {
@@ -42,7 +44,6 @@ namespace {
 constexpr int kRouterThreads = 1024;  // 16 waves
 constexpr int kGroups = 4;            // row groups of 16 rows
 constexpr int kParts = 4;             // quarters of D
-constexpr int kRowsPerWave = kRouterRows / (kRouterThreads / kWave);
 static_assert(kGroups * 16 == kRouterRows, "4 groups of 16 rows per chunk");
 static_assert(kGroups * kParts * kWave == kRouterThreads, "one wave per (group, part)");
 
@@ -89,9 +90,307 @@ __device__ __forceinline__ double wave_sum(double v) {
     return v;
 }
 
-// LDS layout (bytes): logits [64][E] f64, counts [E + 1] int.
+// Logit slots: [64][E + 1] f64 (rows padded by one slot, so that rows read at
+// one expert index spread over the LDS banks).
+__host__ __device__ inline int logit_ld(int E) { return E + 1; }
+
+// LDS layout of router_kernel (bytes): logits [64][E + 1] f64, counts [E + 1] int.
 __host__ __device__ inline size_t router_lds(int E) {
-    return sizeof(double) * (size_t)kRouterRows * E + sizeof(int) * (E + 1);
+    return sizeof(double) * (size_t)kRouterRows * logit_ld(E) + sizeof(int) * (E + 1);
+}
+
+// Reductions over a quad of lanes (4 consecutive lanes) with DPP quad
+// permutes: xor 1 = quad_perm [1,0,3,2] (0xB1), xor 2 = [2,3,0,1] (0x4E).
+template <int CTRL>
+__device__ __forceinline__ int quad_dpp(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+template <int CTRL>
+__device__ __forceinline__ double quad_dpp(double v) {
+    const int64_t b = __double_as_longlong(v);
+    const int lo = quad_dpp<CTRL>((int)(b & 0xffffffff)), hi = quad_dpp<CTRL>((int)(b >> 32));
+    return __longlong_as_double(((int64_t)hi << 32) | (uint32_t)lo);
+}
+__device__ __forceinline__ double quad_max(double v) {
+    v = fmax(v, quad_dpp<0xB1>(v));
+    return fmax(v, quad_dpp<0x4E>(v));
+}
+__device__ __forceinline__ double quad_sum(double v) {
+    v += quad_dpp<0xB1>(v);  // (a + b) + (c + d): the same order in every lane of the quad
+    return v + quad_dpp<0x4E>(v);
+}
+__device__ __forceinline__ double quad_min(double v) {
+    v = fmin(v, quad_dpp<0xB1>(v));
+    return fmin(v, quad_dpp<0x4E>(v));
+}
+__device__ __forceinline__ float quad_maxf(float v) {
+    v = fmaxf(v, __int_as_float(quad_dpp<0xB1>(__float_as_int(v))));
+    return fmaxf(v, __int_as_float(quad_dpp<0x4E>(__float_as_int(v))));
+}
+__device__ __forceinline__ float quad_minf(float v) {
+    v = fminf(v, __int_as_float(quad_dpp<0xB1>(__float_as_int(v))));
+    return fminf(v, __int_as_float(quad_dpp<0x4E>(__float_as_int(v))));
+}
+// The quad's best (value, index): the larger value, and the lower index of
+// equal values (-1 = none).
+__device__ __forceinline__ void quad_argmax(double& bv, int& bi) {
+    auto step = [&](double ov, int oi) {
+        if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
+    };
+    step(quad_dpp<0xB1>(bv), quad_dpp<0xB1>(bi));
+    step(quad_dpp<0x4E>(bv), quad_dpp<0x4E>(bi));
+}
+__device__ __forceinline__ void quad_argmaxf(float& bv, int& bi) {
+    auto step = [&](float ov, int oi) {
+        if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
+    };
+    step(__int_as_float(quad_dpp<0xB1>(__float_as_int(bv))), quad_dpp<0xB1>(bi));
+    step(__int_as_float(quad_dpp<0x4E>(__float_as_int(bv))), quad_dpp<0x4E>(bi));
+}
+
+// k rounds of argmax over a row held by a quad (lane sub: experts sub + L j,
+// bit j of `valid` set where that expert exists), the first maximum winning
+// (the lowest index among equal values); on the logits rounded to f32
+// (f32 = true) or on the f64 logits.  Returns this lane's chosen experts as
+// bits j.
+template <int PL, int L>
+__device__ __forceinline__ uint32_t argmax_rounds(const double (&lv)[PL], uint32_t valid, int k,
+                                                  int sub, bool f32) {
+    uint32_t mine = 0;
+    if (f32) {
+        float lf[PL];
+#pragma unroll
+        for (int j = 0; j < PL; ++j) lf[j] = (float)lv[j];
+        for (int it = 0; it < k; ++it) {
+            const uint32_t open = valid & ~mine;
+            float bv = 0.0f;
+            int bi = -1;
+#pragma unroll
+            for (int j = 0; j < PL; ++j)  // ascending expert: the first maximum stays
+                if (((open >> j) & 1u) && (bi < 0 || lf[j] > bv)) { bv = lf[j]; bi = sub + j * L; }
+            quad_argmaxf(bv, bi);
+            if (bi >= 0 && bi % L == sub) mine |= 1u << (bi / L);
+        }
+    } else {
+        for (int it = 0; it < k; ++it) {
+            const uint32_t open = valid & ~mine;
+            double bv = 0.0;
+            int bi = -1;
+#pragma unroll
+            for (int j = 0; j < PL; ++j)
+                if (((open >> j) & 1u) && (bi < 0 || lv[j] > bv)) { bv = lv[j]; bi = sub + j * L; }
+            quad_argmax(bv, bi);
+            if (bi >= 0 && bi % L == sub) mine |= 1u << (bi / L);
+        }
+    }
+    return mine;
+}
+
+// OR of a 64-bit mask over the quad.
+__device__ __forceinline__ uint64_t quad_or(uint64_t v) {
+    auto step = [&](auto ctrl) {
+        constexpr int C = decltype(ctrl)::value;
+        const uint32_t lo = (uint32_t)quad_dpp<C>((int)(uint32_t)v);
+        const uint32_t hi = (uint32_t)quad_dpp<C>((int)(uint32_t)(v >> 32));
+        v |= ((uint64_t)hi << 32) | lo;
+    };
+    step(std::integral_constant<int, 0xB1>{});
+    step(std::integral_constant<int, 0x4E>{});
+    return v;
+}
+
+// Selection for one chunk of kRouterRows rows from its f64 logits (block of
+// NT threads; every thread calls it): softmax, k rounds of argmax (ties to
+// the lowest index), gates p / (sum_sel p + 1e-9), the k-th/best-unselected
+// logit gap, the dense slot, and the chunk's histogram (s_cnt, zeroed by the
+// caller, written to counts_out).  The logits come in NP partial slot sets
+// [NP][kRouterRows][logit_ld(E)] at s_logit, summed in part order.
+template <int NT, int NP = 1>
+__device__ __forceinline__ void select_chunk(const double* s_logit, int* s_cnt, int64_t chunk_row0,
+                                             int64_t rows, int E, int k, int k_slots,
+                                             float dense_coef, int32_t* __restrict__ topk_idx,
+                                             float* __restrict__ topk_w, float* __restrict__ gap,
+                                             int32_t* __restrict__ counts_out) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int E_cols = E + (k_slots > k ? 1 : 0);
+    const int part_stride = kRouterRows * logit_ld(E);
+    if (E <= kWave) {
+        // Four lanes per row (a DPP quad): lane sub holds experts sub, sub + 4,
+        // ... (at most PL) and their logits in registers; max, sums and argmax
+        // combine over the quad with two DPP quad permutes (xor 1, xor 2).  The
+        // 64 rows take 256 lanes: one pass of a 256-thread block, whole waves
+        // idle past them in a larger block.
+        auto select_rows = [&](auto per_lane) {
+            constexpr int PL = decltype(per_lane)::value;
+            constexpr int L = 4;
+            if (tid >= kRouterRows * L) return;  // whole waves
+            const int lr = tid / L, sub = tid % L;
+            const int64_t orow = chunk_row0 + lr;
+            const bool ok = orow < rows;  // lanes of missing rows still take part
+            const double* lgt = s_logit + (ok ? lr : 0) * logit_ld(E);
+            double lv[PL];
+            uint32_t valid = 0;  // bit j: expert sub + L j exists
+#pragma unroll
+            for (int j = 0; j < PL; ++j) {
+                const int e = sub + j * L;
+                double v = -INFINITY;
+                if (e < E) {
+                    v = lgt[e];
+#pragma unroll
+                    for (int p = 1; p < NP; ++p) v += lgt[p * part_stride + e];
+                    valid |= 1u << j;
+                }
+                lv[j] = v;
+            }
+            double m = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < PL; ++j) m = fmax(m, lv[j]);
+            m = quad_max(m);
+            // exp(l - m) once per expert, in f32 (the difference is taken in
+            // f64): the gates carry about 1e-7 of relative error from it, the
+            // expert choice none (it compares the logits)
+            float pe[PL];
+            double s = 0.0;
+#pragma unroll
+            for (int j = 0; j < PL; ++j) {
+                pe[j] = (valid >> j) & 1u ? expf((float)(lv[j] - m)) : 0.0f;
+                s += (double)pe[j];
+            }
+            s = quad_sum(s);
+            // k rounds of argmax on the logits rounded to f32 (cheaper compares
+            // and half the registers).  f32 rounding is monotonic, so when the
+            // k-th chosen f32 value exceeds the best unchosen one strictly, the
+            // chosen set is the f64 one; otherwise (values within about 1e-7
+            // relative of each other) the rounds run again on the f64 logits.
+            uint32_t mine = argmax_rounds<PL, L>(lv, valid, k, sub, true);  // bit j: chosen
+            float kth32 = INFINITY, un32 = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < PL; ++j) {
+                const float f = (float)lv[j];
+                if ((mine >> j) & 1u) kth32 = fminf(kth32, f);
+                else if ((valid >> j) & 1u) un32 = fmaxf(un32, f);
+            }
+            kth32 = quad_minf(kth32);
+            un32 = quad_maxf(un32);
+            if (!(kth32 > un32)) mine = argmax_rounds<PL, L>(lv, valid, k, sub, false);
+            const double inv_s = 1.0 / s;
+            double kth = INFINITY, best_un = -INFINITY, psel = 0.0;
+            uint64_t sel = 0;  // the row's chosen experts (after the OR over the quad)
+#pragma unroll
+            for (int j = 0; j < PL; ++j) {
+                const bool chosen = (mine >> j) & 1u;
+                psel += chosen ? (double)pe[j] * inv_s : 0.0;
+                kth = chosen ? fmin(kth, lv[j]) : kth;
+                best_un = (!chosen && ((valid >> j) & 1u)) ? fmax(best_un, lv[j]) : best_un;
+                sel |= chosen ? 1ull << (sub + j * L) : 0ull;
+            }
+            kth = quad_min(kth);
+            best_un = quad_max(best_un);
+            psel = quad_sum(psel);
+            sel = quad_or(sel);
+            if (ok) {
+                const double inv_norm = 1.0 / (psel + 1e-9);
+#pragma unroll
+                for (int j = 0; j < PL; ++j) {
+                    if (!((mine >> j) & 1u)) continue;
+                    const int e = sub + j * L;
+                    const int rank = __popcll(sel & ((1ull << e) - 1ull));  // ascending index
+                    topk_idx[orow * k_slots + rank] = e;
+                    topk_w[orow * k_slots + rank] = (float)((double)pe[j] * inv_s * inv_norm);
+                    atomicAdd(&s_cnt[e], 1);
+                }
+                if (sub == 0) {
+                    gap[orow] = (k == E) ? INFINITY : (float)(kth - best_un);
+                    if (k_slots > k) {
+                        topk_idx[orow * k_slots + k] = E;
+                        topk_w[orow * k_slots + k] = dense_coef;
+                        atomicAdd(&s_cnt[E], 1);
+                    }
+                }
+            }
+        };
+        if (E <= 16) select_rows(std::integral_constant<int, 4>{});
+        else select_rows(std::integral_constant<int, 16>{});
+        __syncthreads();
+        for (int e = tid; e < E_cols; e += NT) counts_out[e] = s_cnt[e];
+        return;
+    }
+    constexpr int kRowsPerWave = kRouterRows / (NT / kWave);
+    const int per_lane = (E + kWave - 1) / kWave;  // experts per lane (<= 4 for E <= 256)
+    for (int r = 0; r < kRowsPerWave; ++r) {
+        const int lr = wave * kRowsPerWave + r;
+        const int64_t orow = chunk_row0 + lr;
+        if (orow >= rows) break;  // wave-uniform
+        const double* lgt = s_logit + lr * logit_ld(E);  // (NP == 1 on this path)
+        double m = -INFINITY;
+        for (int j = 0; j < per_lane; ++j) {
+            const int e = lane + j * kWave;
+            if (e < E) m = fmax(m, lgt[e]);
+        }
+        m = wave_max(m);
+        double s = 0.0;
+        for (int j = 0; j < per_lane; ++j) {
+            const int e = lane + j * kWave;
+            if (e < E) s += exp(lgt[e] - m);
+        }
+        s = wave_sum(s);
+
+        uint32_t sel = 0;
+        double kth = INFINITY;
+        for (int it = 0; it < k; ++it) {
+            double bv = 0.0;
+            int bi = -1;
+            for (int j = 0; j < per_lane; ++j) {
+                const int e = lane + j * kWave;
+                if (e < E && !((sel >> j) & 1u)) {
+                    const double lv = lgt[e];
+                    if (bi < 0 || lv > bv) { bv = lv; bi = e; }
+                }
+            }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) {
+                const double ov = __shfl_xor(bv, o);
+                const int oi = __shfl_xor(bi, o);
+                if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
+            }
+            if ((bi & (kWave - 1)) == lane) sel |= 1u << (bi / kWave);
+            kth = bv;
+        }
+        double best_un = -INFINITY, psel = 0.0;
+        for (int j = 0; j < per_lane; ++j) {
+            const int e = lane + j * kWave;
+            if (e >= E) continue;
+            if ((sel >> j) & 1u) psel += exp(lgt[e] - m) / s;
+            else best_un = fmax(best_un, lgt[e]);
+        }
+        best_un = wave_max(best_un);
+        psel = wave_sum(psel);
+
+        int base = 0;
+        for (int j = 0; j < per_lane; ++j) {
+            const bool is_sel = (sel >> j) & 1u;
+            const uint64_t bal = __ballot(is_sel);
+            if (is_sel) {
+                const int e = lane + j * kWave;
+                const int rank = base + __popcll(bal & ((1ull << lane) - 1ull));
+                const double p = exp(lgt[e] - m) / s;
+                topk_idx[orow * k_slots + rank] = e;
+                topk_w[orow * k_slots + rank] = (float)(p / (psel + 1e-9));
+                atomicAdd(&s_cnt[e], 1);
+            }
+            base += __popcll(bal);
+        }
+        if (lane == 0) {
+            gap[orow] = (k == E) ? INFINITY : (float)(kth - best_un);
+            if (k_slots > k) {
+                topk_idx[orow * k_slots + k] = E;
+                topk_w[orow * k_slots + k] = dense_coef;
+                atomicAdd(&s_cnt[E], 1);
+            }
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < E_cols; e += NT) counts_out[e] = s_cnt[e];
 }
 
 // Expert blocks of 16 per pass over x: every x chunk loaded feeds NB MFMAs.
@@ -107,7 +406,7 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
     int k_slots, float dense_coef, int32_t* __restrict__ topk_idx, float* __restrict__ topk_w,
     float* __restrict__ gap, int32_t* __restrict__ chunk_counts) {
     extern __shared__ double s_logit[];                                   // [kRouterRows][E]
-    int* s_cnt = reinterpret_cast<int*>(s_logit + (size_t)kRouterRows * E);  // [E + 1]
+    int* s_cnt = reinterpret_cast<int*>(s_logit + (size_t)kRouterRows * logit_ld(E));  // [E + 1]
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int E_cols = E + (k_slots > k ? 1 : 0);
     for (int e = tid; e < E_cols; e += kRouterThreads) s_cnt[e] = 0;
@@ -205,7 +504,7 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int i = sizeof(T) == 2 ? 4 * lg + r : lg + 4 * r;
-                        double* dst = &s_logit[(g * 16 + i) * E + ex];
+                        double* dst = &s_logit[(g * 16 + i) * logit_ld(E) + ex];
                         *dst = qq == 0 ? c[r] : *dst + c[r];
                     }
                 }
@@ -214,159 +513,182 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
         }
     }
 
-    if (E <= kWave) {
-        // L lanes per row (4 for up to 16 experts: waves 0-3, one per SIMD;
-        // 16 above: all 16 waves): lane sub of a row's group takes experts
-        // sub, sub + L, ...; max, sums and argmax combine over the group with
-        // xor shuffles.
-        auto select_rows = [&](auto lanes) {
-            constexpr int L = decltype(lanes)::value;
-            if (wave >= L) return;
-            const int lr = tid / L, sub = tid % L;
-            const int64_t orow = chunk_row0 + lr;
-            const bool ok = orow < rows;  // lanes of missing rows still shuffle
-            const double* lgt = s_logit + (ok ? lr : 0) * E;
-            auto group_max = [](double v) {
+    select_chunk<kRouterThreads>(s_logit, s_cnt, chunk_row0, rows, E, k, k_slots, dense_coef,
+                                 topk_idx, topk_w, gap, chunk_counts + (int64_t)blockIdx.x * E_cols);
+}
+
+
+// ---- LDS-staged logits: 16-bit inputs, up to 64 experts, D % 128 == 0 -------
+//
+// One block = 4 waves = one chunk of 64 rows.
+//  - x and the router weights stream through an LDS ring of kStages stages,
+//    each 128 elements (256 bytes) of every row of the chunk and of every
+//    expert row.  One direct-to-LDS load fetches 1 KB: four whole 256-byte
+//    row slices, so every HBM line is fetched whole by one instruction.  The
+//    16 chunks of 16 bytes of a slice are stored XOR-swizzled by row bits 0-2
+//    (applied on the global side: lane l always fills slot l), so the 16-row
+//    operand reads of the MFMAs (ds_read_b128) hit distinct banks.
+//  - Wave w takes expert group eg = w % NEG (16 experts) and k part
+//    kp = w / NEG (every NKP-th k step of 32, NKP = 4 / NEG) for all 64 rows:
+//    per k step it reads one weight fragment and four x fragments and runs
+//    four v_mfma_f32_16x16x32 (x as A: lane (r, g) row r, k 8g..8g+7 of the
+//    step; the weights as B with the same k).  Each weight byte of a stage is
+//    read by one wave only, each x byte by NEG waves.
+//  - The MFMA accumulators chain kChain k steps (128 products) in f32 before
+//    each joins an f64 accumulator: the products are exact, each chained
+//    rounding is at most half an ulp of a ~128-term partial sum, so a logit
+//    carries a few 1e-8 of error at unit scale -- far below the 1e-6 near-tie
+//    window that expert choice is checked against.
+//  - The k parts are added into the f64 logit slots in part order (the slots
+//    reuse the ring), then the shared selection runs.
+constexpr int kLdsThreads = 256;
+constexpr int kChain = 4;           // k steps accumulated in f32 per f64 add
+constexpr int kLdsMaxExperts = 64;
+
+// ROWB bytes of each row per stage, NST stages in the ring
+template <typename T, int NEG, int ROWB, int NST>
+__global__ __launch_bounds__(kLdsThreads) void router_lds_kernel(
+    const T* __restrict__ x, const T* __restrict__ wr, int64_t rows, int D, int E, int k,
+    int k_slots, float dense_coef, int32_t* __restrict__ topk_idx, float* __restrict__ topk_w,
+    float* __restrict__ gap, int32_t* __restrict__ chunk_counts) {
+    static_assert(sizeof(T) == 2, "16-bit inputs");
+    constexpr int EPC = 8;                         // elements per 16-byte chunk
+    constexpr int CPR = ROWB / 16;                 // 16-byte chunks per row slice
+    constexpr int KS = CPR * EPC;                  // elements per stage
+    constexpr int RPI = 1024 / ROWB;               // rows per 1 KB load
+    constexpr int NKP = 4 / NEG;                   // k parts
+    constexpr int EP = 16 * NEG;                   // experts, padded to whole groups
+    constexpr int XB = kRouterRows * ROWB;         // x bytes per stage
+    constexpr int SB = XB + EP * ROWB;             // stage bytes
+    constexpr int QX = kRouterRows / RPI / 4;      // x loads per wave per stage
+    constexpr int QW = EP / RPI / 4;               // weight loads per wave per stage
+    constexpr int LPS = QX + QW;                   // loads per wave per stage
+    constexpr int KPW = CPR / 4 / NKP;             // this wave's k steps per stage
+    constexpr int kRing = NST * SB;
+    static_assert(CPR >= 8 && QX >= 1 && QW >= 1 && KPW >= 1, "stage shape");
+    static_assert(NKP * kRouterRows * (16 * NEG + 1) * sizeof(double) <= (size_t)kRing,
+                  "the k parts' logit slots fit in the ring");
+    __shared__ __attribute__((aligned(16))) unsigned char sRing[kRing];
+    __shared__ int s_cnt[kLdsMaxExperts + 1];
+    double* const s_logit = reinterpret_cast<double*>(sRing);  // after the k loop
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int eg = wave % NEG, kp = wave / NEG;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int E_cols = E + (k_slots > k ? 1 : 0);
+    for (int e = tid; e < E_cols; e += kLdsThreads) s_cnt[e] = 0;
+    __syncthreads();  // (before any load is in flight: this barrier may wait for all)
+    const int64_t chunk_row0 = (int64_t)blockIdx.x * kRouterRows;
+    const int nvalid = (int)min<int64_t>(kRouterRows, rows - chunk_row0);
+    const int nstage = D / KS;
+
+    // Load q of a stage fills LDS bytes [q * 1 KB, +1 KB): rows RPI q ..
+    // RPI q + RPI - 1, lane l row RPI q + l / CPR, slot l % CPR holding
+    // logical chunk (l % CPR) ^ (row & 7).  Rows past the chunk re-read its last row, expert
+    // rows past E the last expert (never used).  Byte offsets from the
+    // stage's base (the chunk's first row / expert 0 at that k).
+    uint32_t xoff[QX], woff[QW];
 #pragma unroll
-                for (int o = 1; o < L; o <<= 1) v = fmax(v, __shfl_xor(v, o));
-                return v;
-            };
-            auto group_sum = [](double v) {
-#pragma unroll
-                for (int o = 1; o < L; o <<= 1) v += __shfl_xor(v, o);
-                return v;
-            };
-            double m = -INFINITY;
-            for (int e = sub; e < E; e += L) m = fmax(m, lgt[e]);
-            m = group_max(m);
-            double s = 0.0;
-            for (int e = sub; e < E; e += L) s += exp(lgt[e] - m);
-            s = group_sum(s);
-            uint64_t sel = 0;  // all selected experts of the row (every lane of the group)
-            double kth = INFINITY;
-            for (int it = 0; it < k; ++it) {
-                double bv = 0.0;
-                int bi = -1;
-                for (int e = sub; e < E; e += L)
-                    if (!((sel >> e) & 1ull) && (bi < 0 || lgt[e] > bv)) { bv = lgt[e]; bi = e; }
-#pragma unroll
-                for (int o = 1; o < L; o <<= 1) {  // first maximum wins: lowest index
-                    const double ov = __shfl_xor(bv, o);
-                    const int oi = __shfl_xor(bi, o);
-                    if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
-                }
-                sel |= 1ull << bi;
-                kth = bv;
-            }
-            double best_un = -INFINITY, psel = 0.0;
-            for (int e = sub; e < E; e += L) {
-                if ((sel >> e) & 1ull) psel += exp(lgt[e] - m) / s;
-                else best_un = fmax(best_un, lgt[e]);
-            }
-            best_un = group_max(best_un);
-            psel = group_sum(psel);
-            if (ok) {
-                for (int e = sub; e < E; e += L) {
-                    if (!((sel >> e) & 1ull)) continue;
-                    const int rank = __popcll(sel & ((1ull << e) - 1ull));  // ascending index
-                    const double p = exp(lgt[e] - m) / s;
-                    topk_idx[orow * k_slots + rank] = e;
-                    topk_w[orow * k_slots + rank] = (float)(p / (psel + 1e-9));
-                    atomicAdd(&s_cnt[e], 1);
-                }
-                if (sub == 0) {
-                    gap[orow] = (k == E) ? INFINITY : (float)(kth - best_un);
-                    if (k_slots > k) {
-                        topk_idx[orow * k_slots + k] = E;
-                        topk_w[orow * k_slots + k] = dense_coef;
-                        atomicAdd(&s_cnt[E], 1);
-                    }
-                }
-            }
-        };
-        if (E <= 16) select_rows(std::integral_constant<int, 4>{});
-        else select_rows(std::integral_constant<int, 16>{});
-        __syncthreads();
-        for (int e = tid; e < E_cols; e += kRouterThreads)
-            chunk_counts[(int64_t)blockIdx.x * E_cols + e] = s_cnt[e];
-        return;
+    for (int i = 0; i < QX; ++i) {
+        const int r = (wave * QX + i) * RPI + lane / CPR;
+        const int rr = min(r, nvalid - 1);
+        xoff[i] = (uint32_t)(((int64_t)rr * D + (((lane % CPR) ^ (r & 7)) * EPC)) * 2);
     }
-    const int per_lane = (E + kWave - 1) / kWave;  // experts per lane (<= 4 for E <= 256)
-    for (int r = 0; r < kRowsPerWave; ++r) {
-        const int lr = wave * kRowsPerWave + r;
-        const int64_t orow = chunk_row0 + lr;
-        if (orow >= rows) break;  // wave-uniform
-        const double* lgt = s_logit + lr * E;
-        double m = -INFINITY;
-        for (int j = 0; j < per_lane; ++j) {
-            const int e = lane + j * kWave;
-            if (e < E) m = fmax(m, lgt[e]);
-        }
-        m = wave_max(m);
-        double s = 0.0;
-        for (int j = 0; j < per_lane; ++j) {
-            const int e = lane + j * kWave;
-            if (e < E) s += exp(lgt[e] - m);
-        }
-        s = wave_sum(s);
-
-        uint32_t sel = 0;
-        double kth = INFINITY;
-        for (int it = 0; it < k; ++it) {
-            double bv = 0.0;
-            int bi = -1;
-            for (int j = 0; j < per_lane; ++j) {
-                const int e = lane + j * kWave;
-                if (e < E && !((sel >> j) & 1u)) {
-                    const double lv = lgt[e];
-                    if (bi < 0 || lv > bv) { bv = lv; bi = e; }
-                }
-            }
 #pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) {
-                const double ov = __shfl_xor(bv, o);
-                const int oi = __shfl_xor(bi, o);
-                if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
-            }
-            if ((bi & (kWave - 1)) == lane) sel |= 1u << (bi / kWave);
-            kth = bv;
-        }
-        double best_un = -INFINITY, psel = 0.0;
-        for (int j = 0; j < per_lane; ++j) {
-            const int e = lane + j * kWave;
-            if (e >= E) continue;
-            if ((sel >> j) & 1u) psel += exp(lgt[e] - m) / s;
-            else best_un = fmax(best_un, lgt[e]);
-        }
-        best_un = wave_max(best_un);
-        psel = wave_sum(psel);
+    for (int i = 0; i < QW; ++i) {
+        const int r = (wave * QW + i) * RPI + lane / CPR;
+        const int rr = min(r, E - 1);
+        woff[i] = (uint32_t)(((int64_t)rr * D + (((lane % CPR) ^ (r & 7)) * EPC)) * 2);
+    }
+    const T* const xc = x + chunk_row0 * D;
+    const uint32_t ring = lds_addr(sRing);
+    auto issue = [&](int st, int slot) {
+        const int sc = min(st, nstage - 1);  // past the end: re-load the last stage
+        const uint32_t base = ring + slot * SB;
+#pragma unroll
+        for (int i = 0; i < QX; ++i)
+            lds_dma16(xc + sc * KS, xoff[i], base + (wave * QX + i) * 1024);
+#pragma unroll
+        for (int i = 0; i < QW; ++i)
+            lds_dma16(wr + sc * KS, woff[i], base + XB + (wave * QW + i) * 1024);
+    };
+    // operand fragment: row `row` of a region, logical chunk c
+    auto frag = [&](int slot, int region, int row, int c) -> uint4 {
+        return *reinterpret_cast<const uint4*>(sRing + slot * SB + region + row * ROWB +
+                                              ((c ^ (row & 7)) * 16));
+    };
 
-        int base = 0;
-        for (int j = 0; j < per_lane; ++j) {
-            const bool is_sel = (sel >> j) & 1u;
-            const uint64_t bal = __ballot(is_sel);
-            if (is_sel) {
-                const int e = lane + j * kWave;
-                const int rank = base + __popcll(bal & ((1ull << lane) - 1ull));
-                const double p = exp(lgt[e] - m) / s;
-                topk_idx[orow * k_slots + rank] = e;
-                topk_w[orow * k_slots + rank] = (float)(p / (psel + 1e-9));
-                atomicAdd(&s_cnt[e], 1);
-            }
-            base += __popcll(bal);
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    f4 acc[4];
+    d4 acc64[4];
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+        acc[rg] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        acc64[rg] = d4{0.0, 0.0, 0.0, 0.0};
+    }
+    auto flush = [&]() {
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc64[rg][i] += (double)acc[rg][i];
+            acc[rg] = f4{0.0f, 0.0f, 0.0f, 0.0f};
         }
-        if (lane == 0) {
-            gap[orow] = (k == E) ? INFINITY : (float)(kth - best_un);
-            if (k_slots > k) {
-                topk_idx[orow * k_slots + k] = E;
-                topk_w[orow * k_slots + k] = dense_coef;
-                atomicAdd(&s_cnt[E], 1);
+    };
+#pragma unroll
+    for (int p = 0; p < NST - 1; ++p) issue(p, p);
+    for (int s = 0; s < nstage; ++s) {
+        // this wave's loads of stage s have landed; after the bare barrier
+        // everyone's have, and every wave is done reading stage s - 1 (whose
+        // slot the next load refills).  __syncthreads() would also wait for
+        // the later stages' loads.
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<(NST - 2) * LPS>();
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        issue(s + NST - 1, (s + NST - 1) % NST);
+        const int slot = s % NST;
+#pragma unroll
+        for (int jj = 0; jj < KPW; ++jj) {  // this wave's k steps of the stage
+            const int j = kp + jj * NKP;
+            const uint4 wf = frag(slot, XB, eg * 16 + r16, 4 * j + g);
+#pragma unroll
+            for (int rg = 0; rg < 4; ++rg) {
+                const uint4 xf = frag(slot, 0, rg * 16 + r16, 4 * j + g);
+                typename std::conditional<std::is_same<T, __bf16>::value, bf16x8_t, f16x8_t>::type
+                    av, bv;
+                __builtin_memcpy(&av, &xf, 16);
+                __builtin_memcpy(&bv, &wf, 16);
+                if constexpr (std::is_same<T, __bf16>::value)
+                    acc[rg] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc[rg], 0, 0, 0);
+                else
+                    acc[rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[rg], 0, 0, 0);
+            }
+            // every kChain of this wave's k steps join the f64 accumulators
+            if constexpr (KPW >= kChain) {
+                if ((jj + 1) % kChain == 0) flush();
             }
         }
+        if constexpr (KPW < kChain) {
+            if ((s + 1) % (kChain / KPW) == 0) flush();
+        }
+    }
+    flush();  // the last, partial chain (a no-op add of zeros otherwise)
+    wait_vmcnt<0>();  // the trailing re-loads, before the ring becomes the logit slots
+    __syncthreads();
+    // lane (r16, g) holds expert eg * 16 + r16 of rows rg * 16 + 4 g + i; each
+    // k part fills its own slot set, which the selection adds in part order
+    const int ex = eg * 16 + r16;
+    if (ex < E) {
+        double* part = s_logit + kp * (kRouterRows * logit_ld(E));
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) part[(rg * 16 + 4 * g + i) * logit_ld(E) + ex] = acc64[rg][i];
     }
     __syncthreads();
-    for (int e = tid; e < E_cols; e += kRouterThreads)
-        chunk_counts[(int64_t)blockIdx.x * E_cols + e] = s_cnt[e];
+    select_chunk<kLdsThreads, NKP>(s_logit, s_cnt, chunk_row0, rows, E, k, k_slots, dense_coef,
+                                   topk_idx, topk_w, gap, chunk_counts + (int64_t)blockIdx.x * E_cols);
 }
 
 template <typename T, int NB>
@@ -383,6 +705,17 @@ hipError_t launch_router_nb(const RouterArgs& a, hipStream_t s, int nblk) {
     return hipGetLastError();
 }
 
+template <typename T, int NEG>
+hipError_t launch_router_lds(const RouterArgs& a, hipStream_t s, int nblk) {
+    constexpr int ROWB = 256;
+    constexpr int SB = (kRouterRows + 16 * NEG) * ROWB;    // stage bytes
+    constexpr int NST = std::min(4, (152 * 1024) / SB);     // as deep as the LDS allows
+    hipLaunchKernelGGL((router_lds_kernel<T, NEG, ROWB, NST>), dim3(nblk), dim3(kLdsThreads), 0, s,
+                       (const T*)a.x, (const T*)a.wr, a.rows, a.D, a.E, a.k, a.k_slots,
+                       a.dense_coef, a.topk_idx, a.topk_w, a.gap, a.chunk_counts);
+    return hipGetLastError();
+}
+
 template <typename T>
 hipError_t launch_router_t(const RouterArgs& a, hipStream_t s) {
     const int nblk = (int)((a.rows + kRouterRows - 1) / kRouterRows);
@@ -391,6 +724,12 @@ hipError_t launch_router_t(const RouterArgs& a, hipStream_t s) {
     if constexpr (sizeof(T) == 4) {
         return launch_router_nb<T, 1>(a, s, nblk);
     } else {
+        // LDS-staged logits where they apply (up to 64 experts, D % 128 == 0)
+        if (a.E <= kLdsMaxExperts && a.D % 128 == 0) {
+            if (a.E <= 16) return launch_router_lds<T, 1>(a, s, nblk);
+            if (a.E <= 32) return launch_router_lds<T, 2>(a, s, nblk);
+            return launch_router_lds<T, 4>(a, s, nblk);
+        }
         if (a.E <= 16) return launch_router_nb<T, 1>(a, s, nblk);
         if (a.E <= 32) return launch_router_nb<T, 2>(a, s, nblk);
         return launch_router_nb<T, 4>(a, s, nblk);
