@@ -45,6 +45,14 @@ __device__ __forceinline__ void load16(const T* p, float* out) {
     unpack16<T>(*reinterpret_cast<const uint4*>(p), out);
 }
 
+// A 16-byte store with the nontemporal hint (global_store_dwordx4 ... nt):
+// for streams written once and not read again by the same kernel.
+__device__ __forceinline__ void store16_nt(void* p, const uint4& v) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 t = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(t, reinterpret_cast<u32x4*>(p));
+}
+
 template <typename T>
 __device__ __forceinline__ void store16(T* p, const float* in) {
     Vec16<T> t;

@@ -32,7 +32,7 @@ static_assert(kProdLoads * kProdThreads == kRouterRows * kSlabPieces, "whole sla
 // and the chunk's expert slots), then the int arrays that live to the end.
 constexpr size_t kSlabLds = (size_t)2 * kRouterRows * kSlabStride;
 __host__ __device__ inline size_t dispatch_lds(int E_cols, int k) {
-    return kSlabLds + sizeof(int) * ((size_t)4 * (E_cols + 1) + (size_t)2 * kRouterRows * k);
+    return kSlabLds + sizeof(int) * ((size_t)5 * (E_cols + 1) + (size_t)2 * kRouterRows * k);
 }
 __host__ __device__ inline bool dispatch_fits(int E_cols, int k) {
     return sizeof(int) * ((size_t)2 * kDispWaves * E_cols + (size_t)kRouterRows * k) <= kSlabLds &&
@@ -57,7 +57,12 @@ __host__ __device__ inline bool dispatch_fits(int E_cols, int k) {
 //     consecutive positions: K-blocked, one run of (slots of an expert) x 64
 //     bytes per K-block; row-major, whole 512-byte slab rows.  Producers and
 //     consumers run separate loops with the same barriers, so neither waits
-//     on the other's memory operations.
+//     on the other's memory operations.  The first two slabs are loaded into
+//     the producers' registers during steps 1-3 (slab 0 with step 1's loads,
+//     slab 1 once step 1's values have arrived: steps 2-3 then wait on LDS
+//     only), so the bookkeeping overlaps the copy's first memory latencies.
+//     x_perm is written with the nontemporal hint: the GEMM reads it much
+//     later, from HBM.
 template <typename T, bool kKBlocked>
 __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) {
     extern __shared__ __align__(16) unsigned char s_raw[];
@@ -74,24 +79,70 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
     int* s_ts = s_lb + Ec + 1;                 // [Ec + 1] first tile of expert e
     int* s_prow = s_ts + Ec + 1;               // [64 k] row of the i-th slot in position order
     int* s_ppos = s_prow + kRouterRows * k;    // [64 k] its position
+    int* s_lc = s_ppos + kRouterRows * k;      // [Ec] the chunk's own rows per expert
     int* s_tot = s_red;                        // [Ec] after the reduction (s_red is free)
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int64_t row0 = (int64_t)b * kRouterRows;
     const int nvalid = (int)min<int64_t>(kRouterRows, a.rows - row0);
 
-    // 1. histograms
+    // the copy's geometry (step 4) and the producers' slab loads
+    constexpr int EPC = 16 / sizeof(T);
+    const int nck = a.D / EPC;  // 16-byte chunks per row (D % 8 == 0)
+    const int nslab_all = (nck + kSlabPieces - 1) / kSlabPieces;
+    const int per_part = (nslab_all + parts - 1) / parts;
+    const int sl0 = min(part * per_part, nslab_all);        // this block's first slab
+    const int nslab = min(per_part, nslab_all - sl0);       // and its count (may be 0)
+    const T* __restrict__ x = static_cast<const T*>(a.x);  // x_perm is the layer's own buffer
+    const bool producer = tid < kProdThreads;
+    static_assert(kProdLoads == 4, "four pieces per producer thread");
+    auto fetch = [&](int sl, int u) {  // unconditional: clamped to a valid chunk
+        const int q = tid + u * kProdThreads;
+        const int r = min(q / kSlabPieces, nvalid - 1);
+        const int c = min((sl0 + sl) * kSlabPieces + q % kSlabPieces, nck - 1);
+        return *reinterpret_cast<const uint4*>(x + (row0 + r) * (int64_t)a.D + (int64_t)c * EPC);
+    };
+    // slab 0, in flight with step 1's loads
+    uint4 f0, f1, f2, f3;
+    if (producer) {
+        f0 = fetch(0, 0);
+        f1 = fetch(0, 1);
+        f2 = fetch(0, 2);
+        f3 = fetch(0, 3);
+    }
+
+    // 1. histograms: each wave sums every 16th chunk, 8 chunks' counts in
+    // flight per lane (clamped loads, masked values; a chain of single loads
+    // would pay one cache round trip per 16 chunks)
     for (int e = lane; e < Ec; e += kWave) {
-        int bef = 0, tot = 0;
-        for (int c = wave; c < nch; c += kDispWaves) {
-            const int v = a.chunk_counts[(int64_t)c * Ec + e];
-            tot += v;
-            bef += c < b ? v : 0;
+        int bef = 0, tot = 0, own = 0;
+        for (int c0 = wave; c0 < nch; c0 += 8 * kDispWaves) {
+            int v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                v[u] = a.chunk_counts[(int64_t)min(c0 + u * kDispWaves, nch - 1) * Ec + e];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int c = c0 + u * kDispWaves;
+                const int n = c < nch ? v[u] : 0;
+                tot += n;
+                bef += c < b ? n : 0;
+                own = c == b ? n : own;
+            }
         }
+        if (wave == b % kDispWaves) s_lc[e] = own;
         s_red[wave * Ec + e] = bef;
         s_red[(kDispWaves + wave) * Ec + e] = tot;
     }
     for (int i = tid; i < kRouterRows * k; i += kDispThreads)
         s_idx[i] = (i / k < nvalid) ? a.topk_idx[row0 * k + i] : -1;
+    // slab 1, in flight through steps 2-3 (which read LDS only)
+    uint4 v0, v1, v2, v3;
+    if (producer) {
+        v0 = fetch(1, 0);
+        v1 = fetch(1, 1);
+        v2 = fetch(1, 2);
+        v3 = fetch(1, 3);
+    }
     __syncthreads();
     int my_tot = 0;
     if (tid < Ec) {
@@ -111,7 +162,7 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
         for (int e0 = 0; e0 < Ec; e0 += kWave) {
             const int e = e0 + lane;
             const int v = e < Ec ? s_tot[e] : 0;
-            const int lv = e < Ec ? a.chunk_counts[(int64_t)b * Ec + e] : 0;
+            const int lv = e < Ec ? s_lc[e] : 0;
             const int tv = (v + a.BM - 1) / a.BM;
             int inc = v, linc = lv, tinc = tv;
 #pragma unroll
@@ -184,42 +235,23 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
     }
     __syncthreads();
     // 4. the copy
-    constexpr int EPC = 16 / sizeof(T);
     constexpr int KB = kblock_elems<T>();
     constexpr int kPPK = kKBlockBytes / 16;  // pieces of one row in one K-block
     static_assert(kSlabPieces % kPPK == 0, "a slab holds whole K-blocks");
-    const int nck = a.D / EPC;  // 16-byte chunks per row (D % 8 == 0)
-    const int nslab_all = (nck + kSlabPieces - 1) / kSlabPieces;
-    const int per_part = (nslab_all + parts - 1) / parts;
-    const int sl0 = min(part * per_part, nslab_all);        // this block's first slab
-    const int nslab = min(per_part, nslab_all - sl0);       // and its count (may be 0)
     const int npairs = s_lb[Ec];
-    const T* __restrict__ x = static_cast<const T*>(a.x);  // x_perm is the layer's own buffer
     T* __restrict__ xp = static_cast<T*>(a.x_perm);
-    if (tid < kProdThreads) {
+    if (producer) {
         // producers: slab sl + 1 into LDS while the consumers write slab sl;
         // four 16-byte pieces per thread, in named registers
-        static_assert(kProdLoads == 4, "four pieces per producer thread");
-        auto fetch = [&](int sl, int u) {  // unconditional: clamped to a valid chunk
-            const int q = tid + u * kProdThreads;
-            const int r = min(q / kSlabPieces, nvalid - 1);
-            const int c = min((sl0 + sl) * kSlabPieces + q % kSlabPieces, nck - 1);
-            return *reinterpret_cast<const uint4*>(x + (row0 + r) * (int64_t)a.D + (int64_t)c * EPC);
-        };
         auto stash = [&](int buf, int u, const uint4& v) {
             const int q = tid + u * kProdThreads;
             *reinterpret_cast<uint4*>(slab + (buf * kRouterRows + q / kSlabPieces) * kSlabStride +
                                       (q % kSlabPieces) * 16) = v;
         };
-        uint4 v0 = fetch(0, 0), v1 = fetch(0, 1), v2 = fetch(0, 2), v3 = fetch(0, 3);
-        stash(0, 0, v0);
-        stash(0, 1, v1);
-        stash(0, 2, v2);
-        stash(0, 3, v3);
-        v0 = fetch(1, 0);
-        v1 = fetch(1, 1);
-        v2 = fetch(1, 2);
-        v3 = fetch(1, 3);
+        stash(0, 0, f0);
+        stash(0, 1, f1);
+        stash(0, 2, f2);
+        stash(0, 3, f3);
         __syncthreads();
         for (int sl = 0; sl < nslab; ++sl) {
             const int buf = (sl + 1) & 1;  // slabs past the end are never read
@@ -259,7 +291,7 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
                 const int64_t off = kKBlocked
                     ? ((col / KB) * a.a_cap + p) * KB + col % KB
                     : (int64_t)p * a.D + col;
-                *reinterpret_cast<uint4*>(xp + off) = val;
+                store16_nt(xp + off, val);
             }
             __syncthreads();
         }
