@@ -9,7 +9,7 @@ scan, dispatch, gate/up GEMM, down GEMM, combine) with x already resident in
 HBM.  Prints one JSON line.
 
   python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
-                  [--ffn | --block]
+                  [--ffn | --block | --vendor-gemm]
 """
 from __future__ import annotations
 
@@ -201,6 +201,60 @@ def bench_block(args, w) -> int:
     return 0
 
 
+def bench_vendor_gemm(args, w) -> int:
+    """The vendor GEMM library (hipBLASLt through torch.matmul) on dense GEMMs
+    with the flops of the workload's grouped ones: all A = rows * top_k routed
+    rows against one weight (gate/up: A x D times D x 2H; down: A x H times
+    H x D), operands drawn like the workload's (rows N(0, 1), weights
+    N(0, 1/sqrt(fan_in)), h = silu(g) * u of the gate/up product).  At the
+    chip's power limit the arithmetic rate depends on the operand bits, so the
+    data is matched, not just the shapes.  A same-box yardstick for the grouped
+    GEMMs, not part of the MoE path."""
+    import torch
+
+    T, D, H, k = w.rows, w.dim, w.hidden, w.top_k
+    A = T * k
+    dt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[w.dtype]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(w.base_seed)
+    x = torch.randn(A, D, generator=g, device="cuda").to(dt)
+    w1 = (torch.randn(2 * H, D, generator=g, device="cuda") / D ** 0.5).to(dt)
+    w2 = (torch.randn(D, H, generator=g, device="cuda") / H ** 0.5).to(dt)
+    gu = x @ w1.t()
+    h = (torch.nn.functional.silu(gu[:, :H].float()) * gu[:, H:].float()).to(dt)
+    del gu
+    stream = torch.cuda.current_stream()
+
+    def timed(fn):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(args.steps):
+            fn()
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / args.steps
+
+    out1 = torch.empty(A, 2 * H, dtype=dt, device="cuda")
+    out2 = torch.empty(A, D, dtype=dt, device="cuda")
+    ms1 = timed(lambda: torch.matmul(x, w1.t(), out=out1))
+    ms2 = timed(lambda: torch.matmul(h, w2.t(), out=out2))
+    f1, f2 = 4.0 * A * D * H, 2.0 * A * D * H
+    print(json.dumps({
+        "metric": "vendor GEMM (hipBLASLt via torch.matmul) TFLOP/s on the dense equivalents of "
+                  "the grouped GEMMs",
+        "config": {"workload": f"{w.name}: {w.note}", "routed_rows": A, "dim": D, "hidden": H},
+        "dtype": w.dtype, "steps": args.steps, "warmup": args.warmup,
+        "gate_up": {"shape": [A, 2 * H, D], "ms": ms1, "tflops": f1 / (ms1 * 1e-3) / 1e12,
+                    "frac": f1 / (ms1 * 1e-3) / 1e12 / PEAK_BF16_TFLOPS},
+        "down": {"shape": [A, D, H], "ms": ms2, "tflops": f2 / (ms2 * 1e-3) / 1e12,
+                 "frac": f2 / (ms2 * 1e-3) / 1e12 / PEAK_BF16_TFLOPS},
+    }))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -214,6 +268,9 @@ def main() -> int:
     ap.add_argument("--block", action="store_true",
                     help="time the FFN half of the DiT block (norm2 + modulate, MoE, gated "
                          "residual) against the plain MoE forward")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="time the vendor GEMM library on dense GEMMs with the workload's "
+                         "flops and operand statistics (a yardstick for the grouped GEMMs)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only run a plain copy of this many MB (counter calibration) and exit")
     args = ap.parse_args()
@@ -234,6 +291,8 @@ def main() -> int:
         return bench_ffn(args, w)
     if args.block:
         return bench_block(args, w)
+    if args.vendor_gemm:
+        return bench_vendor_gemm(args, w)
     dt = nm.DataType.of(w.dtype)
     print(f"[bench] workload {w.name}: rows={w.rows} D={w.dim} E={w.experts} k={w.top_k} "
           f"H={w.hidden} {w.dtype}", file=sys.stderr, flush=True)

@@ -438,9 +438,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
             for (int q = tid; q < 2 * kWR * kRowChunks; q += kThreads) {
                 const int sr = q / kRowChunks, ch = q % kRowChunks;
                 const int tr = (sr / kWR) * WM + rd * kWR + sr % kWR;
-                if (tr < nrows)
-                    *reinterpret_cast<uint4*>(out + (int64_t)(row0 + tr) * N + n0 + ch * EPC) =
-                        *reinterpret_cast<const uint4*>(sO + sr * kOS + ch * 16);
+                if (tr < nrows) {
+                    T* dst = out + (int64_t)(row0 + tr) * N + n0 + ch * EPC;
+                    const uint4 v = *reinterpret_cast<const uint4*>(sO + sr * kOS + ch * 16);
+                    if (a.out_nt) store16_nt(dst, v);
+                    else *reinterpret_cast<uint4*>(dst) = v;
+                }
             }
             if (rd < kRounds - 1) {
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");

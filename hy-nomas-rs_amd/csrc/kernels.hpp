@@ -99,7 +99,14 @@ struct GemmArgs {
     // between launches: the last part to arrive resets it)
     float* split_ws;
     int32_t* split_cnt;
+    // down GEMM (MFMA path): write `out` with the nontemporal hint.  For
+    // outputs larger than the chip's last-level cache, which the combine reads
+    // back once: their lines then go to HBM as they are written instead of
+    // being evicted dirty while the combine streams them in.
+    int out_nt = 0;
 };
+// MI355X's last-level cache (the Infinity Cache in front of HBM).
+constexpr int64_t kLastLevelCacheBytes = (int64_t)256 << 20;
 // One split unit's partial tile: 256 x 256 f32.
 constexpr int64_t kSplitUnitFloats = 256 * 256;
 constexpr int kSplitUnits = 256;

@@ -551,6 +551,7 @@ int MoeLayer::run_routed(const void* x, void* y, int64_t rows, hipStream_t s,
     g2.out = w.yperm;
     g2.N = (int)D_;
     g2.K = (int)H_;
+    g2.out_nt = rows * kslots_ * D_ * (int64_t)dtype_size(dt_) > kLastLevelCacheBytes;
     STAGE(mfma_ ? launch_gemm_down_mfma(dt_, g2, s) : launch_gemm_down_simt(dt_, g2, s),
           "down GEMM");
     if ((rc = mark(5))) return rc;
