@@ -432,17 +432,33 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
             }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             __builtin_amdgcn_s_barrier();
-            // staging row sr = (wave half h, row w) holds tile row h * WM + rd * kWR + w
+            // staging row sr = (wave half h, row w) holds tile row h * WM + rd * kWR + w;
+            // 8 pieces per thread at a time: their LDS reads all in flight before
+            // the first store (one read-to-store latency per 8 pieces, not per piece)
             constexpr int kRowChunks = BN * (int)sizeof(T) / 16;
-#pragma unroll 4
-            for (int q = tid; q < 2 * kWR * kRowChunks; q += kThreads) {
-                const int sr = q / kRowChunks, ch = q % kRowChunks;
-                const int tr = (sr / kWR) * WM + rd * kWR + sr % kWR;
-                if (tr < nrows) {
-                    T* dst = out + (int64_t)(row0 + tr) * N + n0 + ch * EPC;
-                    const uint4 v = *reinterpret_cast<const uint4*>(sO + sr * kOS + ch * 16);
-                    if (a.out_nt) store16_nt(dst, v);
-                    else *reinterpret_cast<uint4*>(dst) = v;
+            constexpr int kPieces = 2 * kWR * kRowChunks / kThreads;  // per thread per round
+            constexpr int kGrp = 8;
+            static_assert(kPieces * kThreads == 2 * kWR * kRowChunks && kPieces % kGrp == 0,
+                          "whole groups of pieces per thread");
+#pragma unroll
+            for (int g0 = 0; g0 < kPieces; g0 += kGrp) {
+                uint4 v[kGrp];
+#pragma unroll
+                for (int u = 0; u < kGrp; ++u) {
+                    const int q = tid + (g0 + u) * kThreads;
+                    v[u] = *reinterpret_cast<const uint4*>(sO + (q / kRowChunks) * kOS +
+                                                           (q % kRowChunks) * 16);
+                }
+#pragma unroll
+                for (int u = 0; u < kGrp; ++u) {
+                    const int q = tid + (g0 + u) * kThreads;
+                    const int sr = q / kRowChunks, ch = q % kRowChunks;
+                    const int tr = (sr / kWR) * WM + rd * kWR + sr % kWR;
+                    if (tr < nrows) {
+                        T* dst = out + (int64_t)(row0 + tr) * N + n0 + ch * EPC;
+                        if (a.out_nt) store16_nt(dst, v[u]);
+                        else *reinterpret_cast<uint4*>(dst) = v[u];
+                    }
                 }
             }
             if (rd < kRounds - 1) {
