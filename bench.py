@@ -322,9 +322,10 @@ def main() -> int:
 
     # the headline: K forwards, nothing else on the stream
     ms = timed_steps()
-    # the same K forwards again with the library's per-stage events (each
-    # stage bracketed by HIP events on the forward's stream) for the stage
-    # times and the roofline
+    # the same K forwards again with the library's per-stage events (HIP
+    # events stamped by the runtime at the start and end of each stage's
+    # kernels on the forward's stream: the kernels' own durations) for the
+    # stage times and the roofline
     layer.set_profiling(True)
     ms_profiled = timed_steps()
     stages = layer.stage_times()

@@ -448,7 +448,7 @@ hipError_t launch_dispatch_t(const DispatchArgs& a, hipStream_t s) {
     // grid stays within one block per CU: more blocks than CUs measured slower
     const int nslab = (int)((a.D * sizeof(T) + kSlabBytes - 1) / kSlabBytes);
     const int parts = std::max(1, std::min({kDispCUs / nblk, nslab, kDispMaxParts}));
-    hipLaunchKernelGGL(kern, dim3(nblk * parts), dim3(kDispThreads), lds, s, a);
+    launch_kernel(kern, dim3(nblk * parts), dim3(kDispThreads), lds, s, a);
     return hipGetLastError();
 }
 
@@ -456,9 +456,9 @@ template <typename T>
 hipError_t launch_combine_t(const CombineArgs& a, hipStream_t s) {
     const int nblk = (int)((a.rows + 3) / 4);
     if (a.gate)
-        hipLaunchKernelGGL((combine_kernel<T, true>), dim3(nblk), dim3(256), 0, s, a);
+        launch_kernel((combine_kernel<T, true>), dim3(nblk), dim3(256), 0, s, a);
     else
-        hipLaunchKernelGGL((combine_kernel<T, false>), dim3(nblk), dim3(256), 0, s, a);
+        launch_kernel((combine_kernel<T, false>), dim3(nblk), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -479,7 +479,7 @@ hipError_t launch_dense_tiles(int64_t rows, int BM, int max_tiles, TileInfo* til
                               int32_t* tile_total, hipStream_t s) {
     if (max_tiles <= 0) return hipErrorInvalidValue;
     const int nblk = (max_tiles + 255) / 256;
-    hipLaunchKernelGGL(dense_tiles_kernel, dim3(nblk), dim3(256), 0, s, rows, BM, max_tiles, tiles,
+    launch_kernel(dense_tiles_kernel, dim3(nblk), dim3(256), 0, s, rows, BM, max_tiles, tiles,
                        tile_total);
     return hipGetLastError();
 }
@@ -493,15 +493,15 @@ hipError_t launch_kblock(DType dt, const void* x, void* xk, int64_t rows, int D,
     const unsigned nblk = (unsigned)std::min<int64_t>((chunks + 255) / 256, 65536);
     switch (dt) {
         case DType::BF16:
-            hipLaunchKernelGGL(kblock_kernel<__bf16>, dim3(nblk), dim3(256), 0, s,
+            launch_kernel(kblock_kernel<__bf16>, dim3(nblk), dim3(256), 0, s,
                                (const __bf16*)x, (__bf16*)xk, rows, D, a_cap);
             break;
         case DType::F16:
-            hipLaunchKernelGGL(kblock_kernel<_Float16>, dim3(nblk), dim3(256), 0, s,
+            launch_kernel(kblock_kernel<_Float16>, dim3(nblk), dim3(256), 0, s,
                                (const _Float16*)x, (_Float16*)xk, rows, D, a_cap);
             break;
         case DType::F32:
-            hipLaunchKernelGGL(kblock_kernel<float>, dim3(nblk), dim3(256), 0, s,
+            launch_kernel(kblock_kernel<float>, dim3(nblk), dim3(256), 0, s,
                                (const float*)x, (float*)xk, rows, D, a_cap);
             break;
         default: return hipErrorInvalidValue;

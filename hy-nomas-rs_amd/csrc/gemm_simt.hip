@@ -101,7 +101,7 @@ hipError_t launch_simt_t(const GemmArgs& a, hipStream_t s) {
     const int Nout = MODE == kGateUp ? a.N / 2 : a.N;
     dim3 grid(a.max_tiles, (Nout + kT - 1) / kT);
     if (a.max_tiles <= 0) return hipSuccess;
-    hipLaunchKernelGGL((gemm_simt_kernel<T, MODE>), grid, dim3(256), 0, s, a);
+    launch_kernel((gemm_simt_kernel<T, MODE>), grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -17,6 +17,49 @@
 
 namespace nomas {
 
+// ---- stage timing -----------------------------------------------------------
+// One profiled forward's six stages: stage i's events are ev[2 i] (start) and
+// ev[2 i + 1] (stop), stamped by the runtime at the start of the stage's first
+// kernel and the end of its last one (launch_kernel).  A stage that launches
+// nothing records only its start event (so that later stages still have one to
+// synchronise on) and is flagged in `empty`; its time reads zero.  The
+// destructor leaves no stage in progress on the thread, whatever path the
+// forward returns by.
+constexpr int kProfStages = 6;
+constexpr int kProfEvents = 2 * kProfStages;
+class StageClock {
+public:
+    StageClock(hipEvent_t* ev, uint8_t* empty, hipStream_t s) : ev_(ev), empty_(empty), s_(s) {}
+    ~StageClock() { stage_timing() = nullptr; }
+    StageClock(const StageClock&) = delete;
+    StageClock& operator=(const StageClock&) = delete;
+    // ends stage i - 1 and begins stage i (i == kProfStages: ends the last)
+    hipError_t mark(int i) {
+        if (!ev_) return hipSuccess;
+        stage_timing() = nullptr;
+        if (open_) {
+            empty_[i - 1] = !cur_.launched;
+            if (!cur_.launched) {
+                const hipError_t e = hipEventRecord(cur_.start, s_);
+                if (e != hipSuccess) return e;
+            }
+        }
+        open_ = i < kProfStages;
+        if (open_) {
+            cur_ = StageTiming{ev_[2 * i], ev_[2 * i + 1], false};
+            stage_timing() = &cur_;
+        }
+        return hipSuccess;
+    }
+
+private:
+    hipEvent_t* ev_;
+    uint8_t* empty_;
+    hipStream_t s_;
+    StageTiming cur_{nullptr, nullptr, false};
+    bool open_ = false;
+};
+
 // ---- errors ---------------------------------------------------------------
 // Thread-local last error; functions return a nomas_status code.
 int set_error(int code, const char* fmt, ...);
@@ -237,10 +280,11 @@ private:
     hipEvent_t done_ = nullptr;
     bool done_recorded_ = false;
 
-    // profiling: one set of 7 events per recorded forward
+    // profiling: one set of kProfEvents events per recorded forward
     bool profiling_ = false;
     static constexpr int kRing = 512;
     std::vector<hipEvent_t> events_;
+    std::vector<uint8_t> stage_empty_;  // kProfStages flags per event set
     int recorded_ = 0;
 };
 

@@ -9,11 +9,39 @@
 //   combine -> out[t] = sum over the row's slots (ascending expert) of w * y_perm
 #pragma once
 
+#include <hip/hip_ext.h>
+
 #include "common.hpp"
 
 namespace nomas {
 
 constexpr int kMaxExperts = 256;  // router LDS holds 64 rows x E f64 logits
+
+// Kernel-exact stage timing.  While a layer records a profiled forward, this
+// thread's stage in progress is set here, and every launch of the stage
+// carries its events: the runtime stamps the start event when the stage's
+// first kernel starts and the stop event when each kernel ends (the last one
+// counts).  Null when not profiling.
+struct StageTiming {
+    hipEvent_t start, stop;
+    bool launched;
+};
+StageTiming*& stage_timing();
+
+// Every kernel of the library is launched through here (errors are left for
+// the caller's hipGetLastError).
+template <typename F, typename... Args>
+inline void launch_kernel(F kernel, dim3 grid, dim3 block, uint32_t lds, hipStream_t s,
+                          Args... args) {
+    StageTiming* t = stage_timing();
+    hipEvent_t start = nullptr, stop = nullptr;
+    if (t) {
+        start = t->launched ? nullptr : t->start;
+        stop = t->stop;
+        t->launched = true;
+    }
+    hipExtLaunchKernelGGL(kernel, grid, block, lds, s, start, stop, 0u, args...);
+}
 
 // Tile height (token rows) of the MFMA and of the general grouped GEMM.
 constexpr int kMfmaBM = 256;

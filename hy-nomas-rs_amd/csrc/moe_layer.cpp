@@ -19,6 +19,11 @@
 
 namespace nomas {
 
+StageTiming*& stage_timing() {
+    thread_local StageTiming* t = nullptr;
+    return t;
+}
+
 // ---- errors ---------------------------------------------------------------
 
 namespace {
@@ -453,12 +458,15 @@ int MoeLayer::run_routed(const void* x, void* y, int64_t rows, hipStream_t s,
     const int mt = max_tiles(rows);
     const int64_t a_cap = w.cap_rows * kslots_;
     hipEvent_t* ev = nullptr;
+    uint8_t* empty = nullptr;
     if (profiling_) {
-        ev = &events_[(size_t)(recorded_ % kRing) * 7];
+        ev = &events_[(size_t)(recorded_ % kRing) * kProfEvents];
+        empty = &stage_empty_[(size_t)(recorded_ % kRing) * kProfStages];
         ++recorded_;
     }
+    StageClock clock(ev, empty, s);
     auto mark = [&](int i) -> int {
-        if (ev) HIP_TRY(hipEventRecord(ev[i], s));
+        HIP_TRY(clock.mark(i));
         return NOMAS_OK;
     };
 #define STAGE(call, what)                                                                  \
@@ -583,12 +591,15 @@ int MoeLayer::forward_dense(const void* x, void* y, int64_t rows, hipStream_t s)
     const Workspace& w = ws_;
     const int mt = max_tiles(rows);
     hipEvent_t* ev = nullptr;
+    uint8_t* empty = nullptr;
     if (profiling_) {
-        ev = &events_[(size_t)(recorded_ % kRing) * 7];
+        ev = &events_[(size_t)(recorded_ % kRing) * kProfEvents];
+        empty = &stage_empty_[(size_t)(recorded_ % kRing) * kProfStages];
         ++recorded_;
     }
+    StageClock clock(ev, empty, s);
     auto mark = [&](int i) -> int {
-        if (ev) HIP_TRY(hipEventRecord(ev[i], s));
+        HIP_TRY(clock.mark(i));
         return NOMAS_OK;
     };
 #define STAGE(call, what)                                                                  \
@@ -694,7 +705,8 @@ int MoeLayer::routing(int32_t* idx, float* w, int32_t* counts, float* gap) {
 int MoeLayer::set_profiling(bool on) {
     DeviceGuard g(device_);
     if (on && events_.empty()) {
-        events_.resize((size_t)kRing * 7);
+        events_.resize((size_t)kRing * kProfEvents);
+        stage_empty_.assign((size_t)kRing * kProfStages, 0);
         for (hipEvent_t& e : events_) HIP_TRY(hipEventCreateWithFlags(&e, hipEventReleaseToDevice));
     }
     profiling_ = on;
@@ -711,11 +723,14 @@ int MoeLayer::stage_times(float* ms6) {
     double sum[6] = {0, 0, 0, 0, 0, 0};
     for (int i = 0; i < n; ++i) {
         const int set = (recorded_ - 1 - i) % kRing;
-        hipEvent_t* ev = &events_[(size_t)set * 7];
-        HIP_TRY(hipEventSynchronize(ev[6]));
-        for (int st = 0; st < 6; ++st) {
+        hipEvent_t* ev = &events_[(size_t)set * kProfEvents];
+        const uint8_t* empty = &stage_empty_[(size_t)set * kProfStages];
+        // the last stage's last recorded event
+        HIP_TRY(hipEventSynchronize(ev[empty[kProfStages - 1] ? kProfEvents - 2 : kProfEvents - 1]));
+        for (int st = 0; st < kProfStages; ++st) {
+            if (empty[st]) continue;  // no kernel: zero
             float ms = 0.0f;
-            HIP_TRY(hipEventElapsedTime(&ms, ev[st], ev[st + 1]));
+            HIP_TRY(hipEventElapsedTime(&ms, ev[2 * st], ev[2 * st + 1]));
             sum[st] += ms;
         }
     }

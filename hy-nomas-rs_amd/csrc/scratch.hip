@@ -45,7 +45,7 @@ int scratch_acquire(int device, hipStream_t s, void** out) {
         if (e != hipSuccess || !p)
             return set_error(NOMAS_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d failed: %s",
                              device, hipGetErrorString(e));
-        hipLaunchKernelGGL(clear_counters_kernel, dim3(1), dim3(256), 0, s,
+        launch_kernel(clear_counters_kernel, dim3(1), dim3(256), 0, s,
                            static_cast<int32_t*>(p), kSplitUnits);
         const hipError_t le = hipGetLastError();
         if (le != hipSuccess)

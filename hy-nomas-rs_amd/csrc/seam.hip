@@ -227,7 +227,7 @@ hipError_t launch_seam_h_t(const SeamArgs& a, hipStream_t s) {
     hipError_t err = hipFuncSetAttribute((const void*)seam_h_kernel<T>,
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(seam_h_kernel<T>, dim3((unsigned)nblk), dim3(kSeamThreads), lds, s, b);
+    launch_kernel(seam_h_kernel<T>, dim3((unsigned)nblk), dim3(kSeamThreads), lds, s, b);
     return hipGetLastError();
 }
 
@@ -262,7 +262,7 @@ hipError_t launch_residual_t(const void* x, const void* y, const float* gate, vo
     const int64_t total = rows * (D / (16 / (int)sizeof(T)));
     if (total == 0) return hipSuccess;
     const int64_t blocks = std::min<int64_t>((total + 255) / 256, 256 * 16);
-    hipLaunchKernelGGL(gated_residual_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, s,
+    launch_kernel(gated_residual_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, s,
                        (const T*)x, (const T*)y, gate, (T*)out, rows, D, seq);
     return hipGetLastError();
 }

@@ -161,9 +161,13 @@ int nomas_moe_dims(const nomas_moe_t *h, int64_t *dim, int64_t *hidden, int64_t 
                    int64_t *top_k, int *dtype);
 
 /* Per-stage timing (no reference counterpart; measurement only).  When enabled,
- * each forward records HIP events around its six stages on its stream;
- * nomas_moe_stage_times returns the last forward's durations in milliseconds:
- * [router, scan, dispatch, gemm_gate_up, gemm_down, combine].  Synchronises. */
+ * each forward's kernels carry HIP events that the runtime stamps at the start
+ * of a stage's first kernel and the end of its last, so a stage's time is its
+ * kernels' own (no launch gap); a stage without a kernel reads zero.
+ * nomas_moe_stage_times returns the mean over the forwards recorded since the
+ * last call, in milliseconds: [router, scan, dispatch, gemm_gate_up,
+ * gemm_down, combine] ("scan" is part of the dispatch kernel and reads zero).
+ * Synchronises. */
 int nomas_moe_set_profiling(nomas_moe_t *h, int enable);
 int nomas_moe_stage_times(nomas_moe_t *h, float *ms6);
 

@@ -138,4 +138,4 @@ def test_stage_profiling():
     ffn.set_profiling(False)
     assert set(st) == set(nm.FeedForward.STAGES)
     assert st["gemm_gate_up"] > 0 and st["gemm_down"] > 0
-    assert st["router"] < 0.05 and st["combine"] < 0.05  # no such stages: back-to-back events
+    assert st["router"] == 0 and st["combine"] == 0  # no such stages: no kernel, zero time

@@ -102,9 +102,22 @@ def test_stage_profiling():
     for _ in range(3):
         layer.forward(xd)
     st = layer.stage_times()
-    assert set(st) == set(nm.MoeLayer.STAGES) and all(v > 0 for v in st.values())
+    assert set(st) == set(nm.MoeLayer.STAGES)
+    # the histogram scan runs inside the dispatch kernel: no kernel, zero time
+    assert st["scan"] == 0 and all(v > 0 for k, v in st.items() if k != "scan")
     with pytest.raises(nm.NomasError):
         layer.stage_times()  # nothing recorded since the last read
+    # the stage times are the kernels' own: one forward's add up to no more
+    # than its wall time between two events
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    layer.forward(xd)
+    torch.cuda.synchronize()
+    start.record()
+    layer.forward(xd)
+    end.record()
+    torch.cuda.synchronize()
+    st = layer.stage_times()
+    assert 0 < sum(st.values()) <= start.elapsed_time(end) * 1.001
     layer.set_profiling(False)
 
 
