@@ -131,24 +131,66 @@ __device__ __forceinline__ float quad_minf(float v) {
     v = fminf(v, __int_as_float(quad_dpp<0xB1>(__float_as_int(v))));
     return fminf(v, __int_as_float(quad_dpp<0x4E>(__float_as_int(v))));
 }
+// Reductions over a group of L = 4 or 8 consecutive lanes: the quad steps,
+// then for 8 lanes one exchange with the other quad of the 8 (row_half_mirror:
+// lane i and lane 7 - i).  Every lane of a quad holds the quad's value by
+// then, so the exchange completes the reduction, and a sum's last add has
+// the same two operands in both quads (the same value in all 8 lanes).
+constexpr int kHalfMirror = 0x141;
+template <int L>
+__device__ __forceinline__ double grp_max(double v) {
+    v = quad_max(v);
+    if constexpr (L == 8) v = fmax(v, quad_dpp<kHalfMirror>(v));
+    return v;
+}
+template <int L>
+__device__ __forceinline__ double grp_min(double v) {
+    v = quad_min(v);
+    if constexpr (L == 8) v = fmin(v, quad_dpp<kHalfMirror>(v));
+    return v;
+}
+template <int L>
+__device__ __forceinline__ double grp_sum(double v) {
+    v = quad_sum(v);
+    if constexpr (L == 8) v += quad_dpp<kHalfMirror>(v);
+    return v;
+}
+template <int L>
+__device__ __forceinline__ float grp_maxf(float v) {
+    v = quad_maxf(v);
+    if constexpr (L == 8) v = fmaxf(v, __int_as_float(quad_dpp<kHalfMirror>(__float_as_int(v))));
+    return v;
+}
+template <int L>
+__device__ __forceinline__ float grp_minf(float v) {
+    v = quad_minf(v);
+    if constexpr (L == 8) v = fminf(v, __int_as_float(quad_dpp<kHalfMirror>(__float_as_int(v))));
+    return v;
+}
+
 // The quad's best (value, index): the larger value, and the lower index of
 // equal values (-1 = none).
-__device__ __forceinline__ void quad_argmax(double& bv, int& bi) {
+template <int L>
+__device__ __forceinline__ void grp_argmax(double& bv, int& bi) {
     auto step = [&](double ov, int oi) {
         if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
     };
     step(quad_dpp<0xB1>(bv), quad_dpp<0xB1>(bi));
     step(quad_dpp<0x4E>(bv), quad_dpp<0x4E>(bi));
+    if constexpr (L == 8) step(quad_dpp<kHalfMirror>(bv), quad_dpp<kHalfMirror>(bi));
 }
-__device__ __forceinline__ void quad_argmaxf(float& bv, int& bi) {
+template <int L>
+__device__ __forceinline__ void grp_argmaxf(float& bv, int& bi) {
     auto step = [&](float ov, int oi) {
         if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
     };
     step(__int_as_float(quad_dpp<0xB1>(__float_as_int(bv))), quad_dpp<0xB1>(bi));
     step(__int_as_float(quad_dpp<0x4E>(__float_as_int(bv))), quad_dpp<0x4E>(bi));
+    if constexpr (L == 8)
+        step(__int_as_float(quad_dpp<kHalfMirror>(__float_as_int(bv))), quad_dpp<kHalfMirror>(bi));
 }
 
-// k rounds of argmax over a row held by a quad (lane sub: experts sub + L j,
+// k rounds of argmax over a row held by a group of L lanes (lane sub: experts sub + L j,
 // bit j of `valid` set where that expert exists), the first maximum winning
 // (the lowest index among equal values); on the logits rounded to f32
 // (f32 = true) or on the f64 logits.  Returns this lane's chosen experts as
@@ -168,7 +210,7 @@ __device__ __forceinline__ uint32_t argmax_rounds(const double (&lv)[PL], uint32
 #pragma unroll
             for (int j = 0; j < PL; ++j)  // ascending expert: the first maximum stays
                 if (((open >> j) & 1u) && (bi < 0 || lf[j] > bv)) { bv = lf[j]; bi = sub + j * L; }
-            quad_argmaxf(bv, bi);
+            grp_argmaxf<L>(bv, bi);
             if (bi >= 0 && bi % L == sub) mine |= 1u << (bi / L);
         }
     } else {
@@ -179,15 +221,16 @@ __device__ __forceinline__ uint32_t argmax_rounds(const double (&lv)[PL], uint32
 #pragma unroll
             for (int j = 0; j < PL; ++j)
                 if (((open >> j) & 1u) && (bi < 0 || lv[j] > bv)) { bv = lv[j]; bi = sub + j * L; }
-            quad_argmax(bv, bi);
+            grp_argmax<L>(bv, bi);
             if (bi >= 0 && bi % L == sub) mine |= 1u << (bi / L);
         }
     }
     return mine;
 }
 
-// OR of a 64-bit mask over the quad.
-__device__ __forceinline__ uint64_t quad_or(uint64_t v) {
+// OR of a 64-bit mask over a group of L lanes.
+template <int L>
+__device__ __forceinline__ uint64_t grp_or(uint64_t v) {
     auto step = [&](auto ctrl) {
         constexpr int C = decltype(ctrl)::value;
         const uint32_t lo = (uint32_t)quad_dpp<C>((int)(uint32_t)v);
@@ -196,6 +239,7 @@ __device__ __forceinline__ uint64_t quad_or(uint64_t v) {
     };
     step(std::integral_constant<int, 0xB1>{});
     step(std::integral_constant<int, 0x4E>{});
+    if constexpr (L == 8) step(std::integral_constant<int, kHalfMirror>{});
     return v;
 }
 
@@ -215,14 +259,17 @@ __device__ __forceinline__ void select_chunk(const double* s_logit, int* s_cnt, 
     const int E_cols = E + (k_slots > k ? 1 : 0);
     const int part_stride = kRouterRows * logit_ld(E);
     if (E <= kWave) {
-        // Four lanes per row (a DPP quad): lane sub holds experts sub, sub + 4,
-        // ... (at most PL) and their logits in registers; max, sums and argmax
-        // combine over the quad with two DPP quad permutes (xor 1, xor 2).  The
-        // 64 rows take 256 lanes: one pass of a 256-thread block, whole waves
-        // idle past them in a larger block.
-        auto select_rows = [&](auto per_lane) {
+        // L lanes per row (a DPP quad, or two in blocks of 512 threads or
+        // more): lane sub holds experts sub, sub + L, ... (at most PL) and
+        // their logits in registers; max, sums and argmax combine over the
+        // group with DPP permutes (xor 1, xor 2 and, for 8 lanes, the half-row
+        // mirror).  The 64 rows take 64 L lanes: one pass of a 256- or
+        // 512-thread block, whole waves idle past them in a larger block.
+        // Eight lanes per row halve each lane's dependent chain, and the two
+        // waves per SIMD of a 512-thread block hide each other's latencies.
+        auto select_rows = [&](auto per_lane, auto lanes) {
             constexpr int PL = decltype(per_lane)::value;
-            constexpr int L = 4;
+            constexpr int L = decltype(lanes)::value;
             if (tid >= kRouterRows * L) return;  // whole waves
             const int lr = tid / L, sub = tid % L;
             const int64_t orow = chunk_row0 + lr;
@@ -245,7 +292,7 @@ __device__ __forceinline__ void select_chunk(const double* s_logit, int* s_cnt, 
             double m = -INFINITY;
 #pragma unroll
             for (int j = 0; j < PL; ++j) m = fmax(m, lv[j]);
-            m = quad_max(m);
+            m = grp_max<L>(m);
             // exp(l - m) once per expert, in f32 (the difference is taken in
             // f64): the gates carry about 1e-7 of relative error from it, the
             // expert choice none (it compares the logits)
@@ -256,7 +303,7 @@ __device__ __forceinline__ void select_chunk(const double* s_logit, int* s_cnt, 
                 pe[j] = (valid >> j) & 1u ? expf((float)(lv[j] - m)) : 0.0f;
                 s += (double)pe[j];
             }
-            s = quad_sum(s);
+            s = grp_sum<L>(s);
             // k rounds of argmax on the logits rounded to f32 (cheaper compares
             // and half the registers).  f32 rounding is monotonic, so when the
             // k-th chosen f32 value exceeds the best unchosen one strictly, the
@@ -270,8 +317,8 @@ __device__ __forceinline__ void select_chunk(const double* s_logit, int* s_cnt, 
                 if ((mine >> j) & 1u) kth32 = fminf(kth32, f);
                 else if ((valid >> j) & 1u) un32 = fmaxf(un32, f);
             }
-            kth32 = quad_minf(kth32);
-            un32 = quad_maxf(un32);
+            kth32 = grp_minf<L>(kth32);
+            un32 = grp_maxf<L>(un32);
             if (!(kth32 > un32)) mine = argmax_rounds<PL, L>(lv, valid, k, sub, false);
             const double inv_s = 1.0 / s;
             double kth = INFINITY, best_un = -INFINITY, psel = 0.0;
@@ -284,10 +331,10 @@ __device__ __forceinline__ void select_chunk(const double* s_logit, int* s_cnt, 
                 best_un = (!chosen && ((valid >> j) & 1u)) ? fmax(best_un, lv[j]) : best_un;
                 sel |= chosen ? 1ull << (sub + j * L) : 0ull;
             }
-            kth = quad_min(kth);
-            best_un = quad_max(best_un);
-            psel = quad_sum(psel);
-            sel = quad_or(sel);
+            kth = grp_min<L>(kth);
+            best_un = grp_max<L>(best_un);
+            psel = grp_sum<L>(psel);
+            sel = grp_or<L>(sel);
             if (ok) {
                 const double inv_norm = 1.0 / (psel + 1e-9);
 #pragma unroll
@@ -309,8 +356,15 @@ __device__ __forceinline__ void select_chunk(const double* s_logit, int* s_cnt, 
                 }
             }
         };
-        if (E <= 16) select_rows(std::integral_constant<int, 4>{});
-        else select_rows(std::integral_constant<int, 16>{});
+        if constexpr (NT >= 8 * kRouterRows) {
+            using L8 = std::integral_constant<int, 8>;
+            if (E <= 16) select_rows(std::integral_constant<int, 2>{}, L8{});
+            else select_rows(std::integral_constant<int, 8>{}, L8{});
+        } else {
+            using L4 = std::integral_constant<int, 4>;
+            if (E <= 16) select_rows(std::integral_constant<int, 4>{}, L4{});
+            else select_rows(std::integral_constant<int, 16>{}, L4{});
+        }
         __syncthreads();
         for (int e = tid; e < E_cols; e += NT) counts_out[e] = s_cnt[e];
         return;
@@ -520,7 +574,9 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
 
 // ---- LDS-staged logits: 16-bit inputs, up to 64 experts, D % 128 == 0 -------
 //
-// One block = 4 waves = one chunk of 64 rows.
+// One block = 8 waves = one chunk of 64 rows.  Waves 0-3 compute the logits
+// and load the router weights; waves 4-7 only load x (they take the same
+// barriers).  All 8 waves run the selection, 8 lanes per row.
 //  - x and the router weights stream through an LDS ring of kStages stages,
 //    each 128 elements (256 bytes) of every row of the chunk and of every
 //    expert row.  One direct-to-LDS load fetches 1 KB: four whole 256-byte
@@ -528,7 +584,7 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
 //    16 chunks of 16 bytes of a slice are stored XOR-swizzled by row bits 0-2
 //    (applied on the global side: lane l always fills slot l), so the 16-row
 //    operand reads of the MFMAs (ds_read_b128) hit distinct banks.
-//  - Wave w takes expert group eg = w % NEG (16 experts) and k part
+//  - Compute wave w takes expert group eg = w % NEG (16 experts) and k part
 //    kp = w / NEG (every NKP-th k step of 32, NKP = 4 / NEG) for all 64 rows:
 //    per k step it reads one weight fragment and four x fragments and runs
 //    four v_mfma_f32_16x16x32 (x as A: lane (r, g) row r, k 8g..8g+7 of the
@@ -541,7 +597,8 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
 //    window that expert choice is checked against.
 //  - The k parts are added into the f64 logit slots in part order (the slots
 //    reuse the ring), then the shared selection runs.
-constexpr int kLdsThreads = 256;
+constexpr int kLdsComputeWaves = 4;
+constexpr int kLdsThreads = 2 * kLdsComputeWaves * kWave;  // + 4 waves that load x
 constexpr int kChain = 4;           // k steps accumulated in f32 per f64 add
 constexpr int kLdsMaxExperts = 64;
 
@@ -560,9 +617,8 @@ __global__ __launch_bounds__(kLdsThreads) void router_lds_kernel(
     constexpr int EP = 16 * NEG;                   // experts, padded to whole groups
     constexpr int XB = kRouterRows * ROWB;         // x bytes per stage
     constexpr int SB = XB + EP * ROWB;             // stage bytes
-    constexpr int QX = kRouterRows / RPI / 4;      // x loads per wave per stage
-    constexpr int QW = EP / RPI / 4;               // weight loads per wave per stage
-    constexpr int LPS = QX + QW;                   // loads per wave per stage
+    constexpr int QX = kRouterRows / RPI / 4;      // x loads per loading wave per stage
+    constexpr int QW = EP / RPI / 4;               // weight loads per compute wave per stage
     constexpr int KPW = CPR / 4 / NKP;             // this wave's k steps per stage
     constexpr int kRing = NST * SB;
     static_assert(CPR >= 8 && QX >= 1 && QW >= 1 && KPW >= 1, "stage shape");
@@ -573,7 +629,11 @@ __global__ __launch_bounds__(kLdsThreads) void router_lds_kernel(
     double* const s_logit = reinterpret_cast<double*>(sRing);  // after the k loop
 
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // waves 0-3 compute (and load the weights), waves 4-7 load x; `wave`
+    // numbers each kind 0-3
+    const int wave_all = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool x_loader = wave_all >= kLdsComputeWaves;
+    const int wave = x_loader ? wave_all - kLdsComputeWaves : wave_all;
     const int eg = wave % NEG, kp = wave / NEG;
     const int r16 = lane & 15, g = lane >> 4;
     const int E_cols = E + (k_slots > k ? 1 : 0);
@@ -603,15 +663,18 @@ __global__ __launch_bounds__(kLdsThreads) void router_lds_kernel(
     }
     const T* const xc = x + chunk_row0 * D;
     const uint32_t ring = lds_addr(sRing);
-    auto issue = [&](int st, int slot) {
+    auto issue = [&](int st, int slot) {  // this wave's loads of stage st
         const int sc = min(st, nstage - 1);  // past the end: re-load the last stage
         const uint32_t base = ring + slot * SB;
+        if (x_loader) {
 #pragma unroll
-        for (int i = 0; i < QX; ++i)
-            lds_dma16(xc + sc * KS, xoff[i], base + (wave * QX + i) * 1024);
+            for (int i = 0; i < QX; ++i)
+                lds_dma16(xc + sc * KS, xoff[i], base + (wave * QX + i) * 1024);
+        } else {
 #pragma unroll
-        for (int i = 0; i < QW; ++i)
-            lds_dma16(wr + sc * KS, woff[i], base + XB + (wave * QW + i) * 1024);
+            for (int i = 0; i < QW; ++i)
+                lds_dma16(wr + sc * KS, woff[i], base + XB + (wave * QW + i) * 1024);
+        }
     };
     // operand fragment: row `row` of a region, logical chunk c
     auto frag = [&](int slot, int region, int row, int c) -> uint4 {
@@ -637,13 +700,24 @@ __global__ __launch_bounds__(kLdsThreads) void router_lds_kernel(
     };
 #pragma unroll
     for (int p = 0; p < NST - 1; ++p) issue(p, p);
+    if (x_loader) {
+        // the compute waves' loop without the compute: the same waits and
+        // barriers, so the ring turns in step
+        for (int s = 0; s < nstage; ++s) {
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vmcnt<(NST - 2) * QX>();
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            issue(s + NST - 1, (s + NST - 1) % NST);
+        }
+    } else
     for (int s = 0; s < nstage; ++s) {
         // this wave's loads of stage s have landed; after the bare barrier
         // everyone's have, and every wave is done reading stage s - 1 (whose
         // slot the next load refills).  __syncthreads() would also wait for
         // the later stages' loads.
         __builtin_amdgcn_sched_barrier(0);
-        wait_vmcnt<(NST - 2) * LPS>();
+        wait_vmcnt<(NST - 2) * QW>();
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         issue(s + NST - 1, (s + NST - 1) % NST);
@@ -679,7 +753,7 @@ __global__ __launch_bounds__(kLdsThreads) void router_lds_kernel(
     // lane (r16, g) holds expert eg * 16 + r16 of rows rg * 16 + 4 g + i; each
     // k part fills its own slot set, which the selection adds in part order
     const int ex = eg * 16 + r16;
-    if (ex < E) {
+    if (!x_loader && ex < E) {
         double* part = s_logit + kp * (kRouterRows * logit_ld(E));
 #pragma unroll
         for (int rg = 0; rg < 4; ++rg)
