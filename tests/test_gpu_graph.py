@@ -1,0 +1,79 @@
+"""The forward inside a captured HIP graph.
+
+A forward launches only kernels on the caller's stream once its workspace
+exists (the K-split arrival counters are put back to zero by the kernels that
+use them; nothing is cleared with a memset), so a caller can capture it.  Each
+graph here is replayed several times, with other forwards of the same layer
+(other inputs, other row counts) and host synchronisations between the
+replays, and every replay must equal the eager forward bit for bit.
+"""
+import pytest
+import torch
+
+import nomas_moe as nm
+from nomas_moe import _lib
+from _common import small_case
+from _gpu import to_device
+
+pytestmark = pytest.mark.gpu
+
+PATH = "blocks.0.moe"
+
+
+def _layer(dim, E, k, hidden, dtype, seed):
+    t, _ = small_case(8, dim, E, k, hidden, seed)
+    return nm.MoeLayer.from_source(nm.Weights.from_tensors(t, dtype), PATH, dim, hidden,
+                                   nm.MoeConfig(E, k))
+
+
+def _inputs(rows, dim, dtype, seed):
+    return to_device(nm.randn_affine(seed, rows * dim).reshape(rows, dim), dtype)
+
+
+def _noalloc(layer, x, out):
+    rows = x.numel() // layer.dim
+    rc = _lib.lib().nomas_moe_forward_noalloc(layer._h, x.data_ptr(), out.data_ptr(), rows,
+                                              torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, _lib.last_error()
+
+
+@pytest.mark.parametrize("entry", ["forward", "forward_noalloc"])
+@pytest.mark.parametrize("dim,E,k,hidden,dtype,rows", [
+    (256, 8, 2, 256, "bf16", 1500),   # MFMA path
+    (256, 8, 2, 128, "f32", 700),     # MFMA path, f32
+    (192, 4, 2, 96, "bf16", 400),     # general grouped GEMM
+])
+def test_graph_replays_match_eager(entry, dim, E, k, hidden, dtype, rows):
+    layer = _layer(dim, E, k, hidden, dtype, 90 + rows % 7)
+    run = (lambda x, y: layer.forward(x, out=y)) if entry == "forward" else \
+        (lambda x, y: _noalloc(layer, x, y))
+    x = _inputs(rows, dim, dtype, 1)
+    other = _inputs(rows // 2 + 3, dim, dtype, 2)
+    y = torch.empty_like(x)
+    y_other = torch.empty_like(other)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        run(x, y)             # the workspace exists before the capture
+        run(other, y_other)
+    torch.cuda.synchronize()
+    eager = y.clone()
+    eager_other = y_other.clone()
+
+    g = torch.cuda.CUDAGraph()
+    y.zero_()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=s):
+        run(x, y)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager), f"replay {rep} differs from the eager forward"
+        # the program's own eager work between replays: another forward of
+        # the same layer on other rows, which reuses the same buffers
+        with torch.cuda.stream(s):
+            run(other, y_other)
+        torch.cuda.synchronize()
+        assert torch.equal(y_other, eager_other)
