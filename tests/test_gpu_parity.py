@@ -157,8 +157,9 @@ def test_exact_ties_go_to_the_lowest_index(E):
                                        (48, 6, "bf16"), (64, 8, "f16"), (65, 8, "bf16")])
 def test_router_pass_widths(E, k, dtype):
     # one pass over x covers 16, 32 or 64 experts (E <= 16, <= 32, more), with
-    # partly filled 16-expert blocks; the selection takes 4 lanes per row up to
-    # 16 experts, 16 lanes up to 64, the whole wave beyond
+    # partly filled 16-expert blocks; the selection takes 8 lanes per row up to
+    # 64 experts (2 candidates per lane up to 16 experts, 8 beyond), the whole
+    # wave per row past 64
     run_case(330, 256, E, k, 128, dtype, seed=40 + E, router_std=0.2)
 
 
