@@ -480,7 +480,7 @@ hipError_t launch_dense_tiles(int64_t rows, int BM, int max_tiles, TileInfo* til
     if (max_tiles <= 0) return hipErrorInvalidValue;
     const int nblk = (max_tiles + 255) / 256;
     launch_kernel(dense_tiles_kernel, dim3(nblk), dim3(256), 0, s, rows, BM, max_tiles, tiles,
-                       tile_total);
+                  tile_total);
     return hipGetLastError();
 }
 
@@ -494,15 +494,15 @@ hipError_t launch_kblock(DType dt, const void* x, void* xk, int64_t rows, int D,
     switch (dt) {
         case DType::BF16:
             launch_kernel(kblock_kernel<__bf16>, dim3(nblk), dim3(256), 0, s,
-                               (const __bf16*)x, (__bf16*)xk, rows, D, a_cap);
+                          (const __bf16*)x, (__bf16*)xk, rows, D, a_cap);
             break;
         case DType::F16:
             launch_kernel(kblock_kernel<_Float16>, dim3(nblk), dim3(256), 0, s,
-                               (const _Float16*)x, (_Float16*)xk, rows, D, a_cap);
+                          (const _Float16*)x, (_Float16*)xk, rows, D, a_cap);
             break;
         case DType::F32:
             launch_kernel(kblock_kernel<float>, dim3(nblk), dim3(256), 0, s,
-                               (const float*)x, (float*)xk, rows, D, a_cap);
+                          (const float*)x, (float*)xk, rows, D, a_cap);
             break;
         default: return hipErrorInvalidValue;
     }

@@ -482,7 +482,7 @@ hipError_t launch_mfma_t(const GemmArgs& a, hipStream_t s) {
     if (a.max_tiles <= 0) return hipSuccess;
     if (grid > 0x7fffffff) return hipErrorInvalidValue;
     launch_kernel((gemm_mfma_kernel<T, MODE, BM, BN, BK, kStages>), dim3((unsigned)grid),
-                       dim3(kThreads), 0, s, a);
+                  dim3(kThreads), 0, s, a);
     return hipGetLastError();
 }
 

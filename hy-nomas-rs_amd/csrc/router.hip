@@ -774,8 +774,8 @@ hipError_t launch_router_nb(const RouterArgs& a, hipStream_t s, int nblk) {
         if (err != hipSuccess) return err;
     }
     launch_kernel((router_kernel<T, NB>), dim3(nblk), dim3(kRouterThreads), lds, s,
-                       (const T*)a.x, (const T*)a.wr, a.rows, a.D, a.E, a.k, a.k_slots,
-                       a.dense_coef, a.topk_idx, a.topk_w, a.gap, a.chunk_counts);
+                  (const T*)a.x, (const T*)a.wr, a.rows, a.D, a.E, a.k, a.k_slots,
+                  a.dense_coef, a.topk_idx, a.topk_w, a.gap, a.chunk_counts);
     return hipGetLastError();
 }
 
@@ -785,8 +785,8 @@ hipError_t launch_router_lds(const RouterArgs& a, hipStream_t s, int nblk) {
     constexpr int SB = (kRouterRows + 16 * NEG) * ROWB;    // stage bytes
     constexpr int NST = std::min(4, (152 * 1024) / SB);     // as deep as the LDS allows
     launch_kernel((router_lds_kernel<T, NEG, ROWB, NST>), dim3(nblk), dim3(kLdsThreads), 0, s,
-                       (const T*)a.x, (const T*)a.wr, a.rows, a.D, a.E, a.k, a.k_slots,
-                       a.dense_coef, a.topk_idx, a.topk_w, a.gap, a.chunk_counts);
+                  (const T*)a.x, (const T*)a.wr, a.rows, a.D, a.E, a.k, a.k_slots,
+                  a.dense_coef, a.topk_idx, a.topk_w, a.gap, a.chunk_counts);
     return hipGetLastError();
 }
 

@@ -46,7 +46,7 @@ int scratch_acquire(int device, hipStream_t s, void** out) {
             return set_error(NOMAS_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d failed: %s",
                              device, hipGetErrorString(e));
         launch_kernel(clear_counters_kernel, dim3(1), dim3(256), 0, s,
-                           static_cast<int32_t*>(p), kSplitUnits);
+                      static_cast<int32_t*>(p), kSplitUnits);
         const hipError_t le = hipGetLastError();
         if (le != hipSuccess)
             return set_error(NOMAS_ERR_HIP, "clearing the scratch counters failed: %s",

@@ -263,7 +263,7 @@ hipError_t launch_residual_t(const void* x, const void* y, const float* gate, vo
     if (total == 0) return hipSuccess;
     const int64_t blocks = std::min<int64_t>((total + 255) / 256, 256 * 16);
     launch_kernel(gated_residual_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, s,
-                       (const T*)x, (const T*)y, gate, (T*)out, rows, D, seq);
+                  (const T*)x, (const T*)y, gate, (T*)out, rows, D, seq);
     return hipGetLastError();
 }
 
