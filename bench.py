@@ -9,7 +9,7 @@ scan, dispatch, gate/up GEMM, down GEMM, combine) with x already resident in
 HBM.  Prints one JSON line.
 
   python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
-                  [--ffn | --block | --vendor-gemm]
+                  [--ffn | --block | --vendor-gemm | --hbm-yardstick]
 """
 from __future__ import annotations
 
@@ -255,6 +255,65 @@ def bench_vendor_gemm(args, w) -> int:
     return 0
 
 
+def bench_hbm_yardstick(args, w) -> int:
+    """torch's own elementwise and reduction kernels moving the bytes of the
+    dispatch and the combine at the workload's shape, as a same-box yardstick
+    for what the memory system sustains on such traffic:
+      - broadcast copy: x (T x D) written k times into a (T*k) x D buffer, the
+        dispatch's byte mix with contiguous instead of routed writes;
+      - sum over k: (T, k, D) summed over k into T x D, the combine's byte mix
+        with contiguous instead of routed reads (bf16 in, f32 sums, bf16 out);
+      - fill, read (a full sum) and copy of the (T*k) x D buffer: pure writes,
+        pure reads, and reads plus writes of the routed rows' bytes.
+    Bytes are counted like the dispatch's and combine's algorithmic bytes.  Not
+    part of the MoE path."""
+    import torch
+
+    T, D, k = w.rows, w.dim, w.top_k
+    A = T * k
+    dt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[w.dtype]
+    b = torch.tensor([], dtype=dt).element_size()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(w.base_seed)
+    x = torch.randn(T, D, generator=g, device="cuda").to(dt)
+    xe = torch.randn(A, D, generator=g, device="cuda").to(dt)
+    xe2 = torch.empty_like(xe)
+    out = torch.empty(T, D, dtype=dt, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def timed(fn):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(args.steps):
+            fn()
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / args.steps
+
+    cases = {
+        "broadcast_copy": (lambda: xe.view(T, k, D).copy_(x.unsqueeze(1).expand(T, k, D)),
+                           T * D * b + A * D * b),
+        "sum_over_k": (lambda: torch.sum(xe.view(T, k, D), dim=1, out=out), A * D * b + T * D * b),
+        "fill": (lambda: xe2.fill_(1.0), A * D * b),
+        "read": (lambda: xe.sum(), A * D * b),
+        "copy": (lambda: xe2.copy_(xe), 2 * A * D * b),
+    }
+    res = {}
+    for name, (fn, nbytes) in cases.items():
+        ms = timed(fn)
+        tbs = nbytes / (ms * 1e-3) / 1e12
+        res[name] = {"us": ms * 1e3, "bytes": nbytes, "TB/s": tbs, "frac": tbs * 1e3 / PEAK_HBM_GBPS}
+    print(json.dumps({
+        "metric": "torch kernels' HBM rate on the dispatch's and combine's byte mix (yardstick)",
+        "config": {"workload": f"{w.name}: {w.note}", "rows": T, "dim": D, "top_k": k},
+        "dtype": w.dtype, "steps": args.steps, "warmup": args.warmup, "cases": res,
+    }))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -271,6 +330,9 @@ def main() -> int:
     ap.add_argument("--vendor-gemm", action="store_true",
                     help="time the vendor GEMM library on dense GEMMs with the workload's "
                          "flops and operand statistics (a yardstick for the grouped GEMMs)")
+    ap.add_argument("--hbm-yardstick", action="store_true",
+                    help="time torch's own kernels on the dispatch's and combine's byte mix "
+                         "(a yardstick for the memory-bound stages)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only run a plain copy of this many MB (counter calibration) and exit")
     args = ap.parse_args()
@@ -293,6 +355,8 @@ def main() -> int:
         return bench_block(args, w)
     if args.vendor_gemm:
         return bench_vendor_gemm(args, w)
+    if args.hbm_yardstick:
+        return bench_hbm_yardstick(args, w)
     dt = nm.DataType.of(w.dtype)
     print(f"[bench] workload {w.name}: rows={w.rows} D={w.dim} E={w.experts} k={w.top_k} "
           f"H={w.hidden} {w.dtype}", file=sys.stderr, flush=True)

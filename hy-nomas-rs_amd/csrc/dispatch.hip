@@ -47,7 +47,7 @@ __host__ __device__ inline bool dispatch_fits(int E_cols, int k) {
 //     own per-expert slot offsets; block 0 also publishes the expert counts
 //     and offsets and the GEMM tile table (ceil(count / BM) tiles of BM rows
 //     per expert);
-//  3. wave 0 ranks the chunk's slots: for each expert in ascending order, a
+//  3. the waves rank the chunk's slots, each taking every 16th expert: a
 //     ballot over the 64 rows gives every row its rank among the chunk's rows
 //     of that expert; base + rank is a stable position.  The slots are listed
 //     in position order (expert, then row), positions increasing;
@@ -110,18 +110,19 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
         f3 = fetch(0, 3);
     }
 
-    // 1. histograms: each wave sums every 16th chunk, 8 chunks' counts in
+    // 1. histograms: each wave sums every 16th chunk, 16 chunks' counts in
     // flight per lane (clamped loads, masked values; a chain of single loads
-    // would pay one cache round trip per 16 chunks)
+    // would pay one cache round trip per 16 chunks): one round trip up to 256
+    // chunks
     for (int e = lane; e < Ec; e += kWave) {
         int bef = 0, tot = 0, own = 0;
-        for (int c0 = wave; c0 < nch; c0 += 8 * kDispWaves) {
-            int v[8];
+        for (int c0 = wave; c0 < nch; c0 += 16 * kDispWaves) {
+            int v[16];
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
+            for (int u = 0; u < 16; ++u)
                 v[u] = a.chunk_counts[(int64_t)min(c0 + u * kDispWaves, nch - 1) * Ec + e];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
+            for (int u = 0; u < 16; ++u) {
                 const int c = c0 + u * kDispWaves;
                 const int n = c < nch ? v[u] : 0;
                 tot += n;
@@ -215,21 +216,45 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
             a.tiles[i] = t;
         }
     }
-    // 3. ranks and positions
-    if (wave == 0) {
-        const int* mine = s_idx + lane * k;
-        int cur = 0;
-        for (int e = 0; e < Ec; ++e) {
-            const bool has = cur < k && mine[cur] == e;
+    // 3. ranks and positions.  Every wave holds each row's experts as a bit
+    // set (lane = row); a row's slots hold distinct experts in ascending
+    // order, so the slot of expert e is the number of the row's experts below
+    // e.  The waves take the experts in turn (wave w: w, w + 16, ...), and
+    // one ballot over the chunk's rows ranks expert e's slots.
+    {
+        constexpr int kSetWords = (kMaxExperts + 1 + 63) / 64;
+        uint64_t eset[kSetWords];
+#pragma unroll
+        for (int w = 0; w < kSetWords; ++w) eset[w] = 0;
+        for (int t = 0; t < k; ++t) {
+            const int e = s_idx[lane * k + t];  // -1 past the chunk's rows
+#pragma unroll
+            for (int w = 0; w < kSetWords; ++w)
+                if (e >= 0 && (e >> 6) == w) eset[w] |= 1ull << (e & 63);
+        }
+        int below[kSetWords];  // the row's experts in the words before word w
+        below[0] = 0;
+#pragma unroll
+        for (int w = 1; w < kSetWords; ++w) below[w] = below[w - 1] + __popcll(eset[w - 1]);
+        for (int e = wave; e < Ec; e += kDispWaves) {
+            uint64_t word = 0;
+            int j = 0;
+#pragma unroll
+            for (int w = 0; w < kSetWords; ++w)
+                if ((e >> 6) == w) {
+                    word = eset[w];
+                    j = below[w];
+                }
+            const bool has = (word >> (e & 63)) & 1ull;
             const uint64_t bal = __ballot(has);
             if (has) {
+                j += __popcll(word & ((1ull << (e & 63)) - 1ull));
                 const int rank = __popcll(bal & ((1ull << lane) - 1ull));
                 const int p = s_off[e] + s_bef[e] + rank;
                 const int li = s_lb[e] + rank;
                 s_prow[li] = lane;
                 s_ppos[li] = p;
-                if (part == 0) a.tok_pos[(row0 + lane) * k + cur] = p;
-                ++cur;
+                if (part == 0) a.tok_pos[(row0 + lane) * k + j] = p;
             }
         }
     }
@@ -267,31 +292,54 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
         }
     } else {
         // consumers
+        constexpr int kCons = kDispThreads - kProdThreads;
         const int ct = tid - kProdThreads;
-        const int npieces = npairs * kSlabPieces;
         __syncthreads();
         for (int sl = 0; sl < nslab; ++sl) {
             const unsigned char* sb = slab + (sl & 1) * kRouterRows * kSlabStride;
-            for (int v = ct; v < npieces; v += kDispThreads - kProdThreads) {
-                int pr, h;
-                if constexpr (kKBlocked) {  // (K-block, slot, piece): runs along positions
-                    const int per_kb = npairs * kPPK;
-                    const int kbl = v / per_kb, rem = v - kbl * per_kb;
-                    pr = rem / kPPK;
-                    h = kbl * kPPK + rem % kPPK;
-                } else {  // (slot, piece): whole slab rows
-                    pr = v / kSlabPieces;
-                    h = v % kSlabPieces;
+            if constexpr (kKBlocked) {
+                // A thread owns piece ct % kPPK of slots ct / kPPK, + kCons / kPPK,
+                // ...: for each, one position and row lookup, then the slab's
+                // K-blocks of that piece, their LDS reads all in flight before
+                // the stores (a_cap * KB elements apart).  Lanes 4i..4i+3 write
+                // slot i's 64 bytes of a K-block: one store instruction covers
+                // 16 consecutive positions.  (The slab holds whole K-blocks:
+                // the K-blocked layout needs D % KB == 0.)
+                constexpr int kKbs = kSlabPieces / kPPK;  // K-blocks per slab
+                const int piece = ct % kPPK;
+                const int kb0 = (sl0 + sl) * kKbs;
+                const int nkb = min(kKbs, nck / kPPK - kb0);
+                const int64_t kstep = a.a_cap * KB;
+                for (int pr = ct / kPPK; pr < npairs; pr += kCons / kPPK) {
+                    const int p = s_ppos[pr];
+                    if (p < 0 || p >= a.a_cap) continue;
+                    const unsigned char* src = sb + s_prow[pr] * kSlabStride + piece * 16;
+                    T* dst = xp + ((int64_t)kb0 * a.a_cap + p) * KB + piece * EPC;
+                    if (nkb == kKbs) {
+                        uint4 val[kKbs];
+#pragma unroll
+                        for (int q = 0; q < kKbs; ++q)
+                            val[q] = *reinterpret_cast<const uint4*>(src + q * kKBlockBytes);
+#pragma unroll
+                        for (int q = 0; q < kKbs; ++q) store16_nt(dst + q * kstep, val[q]);
+                    } else {
+                        for (int q = 0; q < nkb; ++q)
+                            store16_nt(dst + q * kstep,
+                                       *reinterpret_cast<const uint4*>(src + q * kKBlockBytes));
+                    }
                 }
-                const int c = (sl0 + sl) * kSlabPieces + h;
-                const int p = s_ppos[pr];
-                if (c >= nck || p < 0 || p >= a.a_cap) continue;
-                const uint4 val = *reinterpret_cast<const uint4*>(sb + s_prow[pr] * kSlabStride + h * 16);
-                const int64_t col = (int64_t)c * EPC;
-                const int64_t off = kKBlocked
-                    ? ((col / KB) * a.a_cap + p) * KB + col % KB
-                    : (int64_t)p * a.D + col;
-                store16_nt(xp + off, val);
+            } else {
+                // (slot, piece): whole 512-byte slab rows
+                const int npieces = npairs * kSlabPieces;
+                for (int v = ct; v < npieces; v += kCons) {
+                    const int pr = v / kSlabPieces, h = v % kSlabPieces;
+                    const int c = (sl0 + sl) * kSlabPieces + h;
+                    const int p = s_ppos[pr];
+                    if (c >= nck || p < 0 || p >= a.a_cap) continue;
+                    const uint4 val =
+                        *reinterpret_cast<const uint4*>(sb + s_prow[pr] * kSlabStride + h * 16);
+                    store16_nt(xp + (int64_t)p * a.D + (int64_t)c * EPC, val);
+                }
             }
             __syncthreads();
         }
@@ -435,7 +483,8 @@ hipError_t launch_dispatch_t(const DispatchArgs& a, hipStream_t s) {
     const int nblk = (int)((a.rows + kRouterRows - 1) / kRouterRows);
     if (nblk == 0) return hipSuccess;
     if (a.nchunks != nblk || a.E_cols < 1 || a.E_cols > kMaxExperts + 1 || a.k_slots < 1 ||
-        a.k_slots > a.E_cols || a.BM < 1 || !dispatch_fits(a.E_cols, a.k_slots))
+        a.k_slots > a.E_cols || a.BM < 1 || !dispatch_fits(a.E_cols, a.k_slots) ||
+        (a.kblocked && (int64_t)a.D * (int64_t)sizeof(T) % kKBlockBytes != 0))
         return hipErrorInvalidValue;
     const size_t lds = dispatch_lds(a.E_cols, a.k_slots);
     // the x_perm layout as a compile-time choice: no layout test in the copy loop
