@@ -200,6 +200,8 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
         if (tid == 0) {
             a.expert_off[Ec] = s_off[Ec];
             a.tile_total[0] = min(total_tiles, a.max_tiles);
+            a.tile_total[1] = 0;  // the GEMMs' tail counters
+            a.tile_total[2] = 0;
         }
         for (int i = tid; i < total_tiles && i < a.max_tiles; i += kDispThreads) {
             int lo = 0, hi = Ec - 1;  // last expert with s_ts <= i (skipping empty ones)
@@ -457,7 +459,11 @@ __global__ void dense_tiles_kernel(int64_t rows, int BM, int max_tiles, TileInfo
         t.pad = 0;
         tiles[i] = t;
     }
-    if (blockIdx.x == 0 && threadIdx.x == 0) *tile_total = (int32_t)min<int64_t>(ntiles, max_tiles);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        tile_total[0] = (int32_t)min<int64_t>(ntiles, max_tiles);
+        tile_total[1] = 0;  // the GEMMs' tail counters
+        tile_total[2] = 0;
+    }
 }
 
 // x (rows x D, row-major) to the K-blocked layout of the MFMA GEMMs: one

@@ -127,10 +127,21 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
 
     const int N = a.N, K = a.K;
     const int KT_tile = K / BK;  // k steps of a whole tile
-    // live row tiles (the dispatch never lists more than max_tiles)
+    // live row tiles (the dispatch never lists more than max_tiles); the
+    // block's unit: by its time-order index, or in the tail a ticket's
     const int live = min(*a.tile_total, a.max_tiles);
+    const long long units = unit_count(live, N / BN, KT_tile / S), first_tail = tail_start(units);
+    long long L = time_order(blockIdx.x);
+    if (L >= first_tail) {
+        __shared__ int s_ticket;
+        if (threadIdx.x == 0)
+            s_ticket = __hip_atomic_fetch_add(a.tail_cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        L = first_tail + s_ticket;
+        if (L >= units) return;
+    }
     WorkUnit wu;
-    if (!unit_coords(blockIdx.x, N / BN, live, KT_tile / S, &wu)) return;
+    unit_at(L, N / BN, live, KT_tile / S, &wu);
     const int mt = wu.mt, nt = wu.nt;
     const TileInfo ti = a.tiles[mt];
     const int e = ti.expert, row0 = ti.row0, nrows = ti.rows;
@@ -475,7 +486,8 @@ hipError_t launch_mfma_t(const GemmArgs& a, hipStream_t s) {
     // whole column tiles, and whole turns of the ring in K
     constexpr int BK = kblock_elems<T>();
     if (a.N % BN != 0 || a.K % (BK * kStages) != 0) return hipErrorInvalidValue;
-    if (a.split_ws == nullptr || a.split_cnt == nullptr) return hipErrorInvalidValue;
+    if (a.split_ws == nullptr || a.split_cnt == nullptr || a.tail_cnt == nullptr)
+        return hipErrorInvalidValue;
     // whole tiles, plus one round for the K-split units of a short last round
     static_assert(kSplitUnits == kRound, "the split units fill one round");
     const int64_t grid = tile_grid(a.max_tiles, a.N / BN) + kSplitUnits;

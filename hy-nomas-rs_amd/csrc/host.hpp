@@ -147,7 +147,7 @@ struct Workspace {
     int32_t* expert_count = nullptr; // E_cols
     int32_t* expert_off = nullptr;   // E_cols + 1
     TileInfo* tiles = nullptr;       // max_tiles
-    int32_t* tile_total = nullptr;   // 1
+    int32_t* tile_total = nullptr;   // 3: tile count, the GEMMs' tail counters
     void* xperm = nullptr;           // a_cap x D
     void* h = nullptr;               // a_cap x H
     void* yperm = nullptr;           // a_cap x D (MoE only)

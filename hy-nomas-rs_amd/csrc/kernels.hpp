@@ -103,7 +103,7 @@ struct DispatchArgs {
     int32_t* expert_count;  // E_cols
     int32_t* expert_off;    // E_cols + 1
     TileInfo* tiles;        // max_tiles
-    int32_t* tile_total;    // 1
+    int32_t* tile_total;    // 3: the tile count, then the two GEMMs' tail counters (cleared)
     int32_t* tok_pos;  // rows x k_slots
     void* x_perm;      // a_cap x D, row-major or K-blocked
     int64_t a_cap;     // rows of x_perm (positions must stay below)
@@ -127,6 +127,9 @@ struct GemmArgs {
     // between launches: the last part to arrive resets it)
     float* split_ws;
     int32_t* split_cnt;
+    // MFMA path: the ticket counter of the tail units handed out at run time
+    // (zero before the launch: the kernel that writes the tile table clears it)
+    int32_t* tail_cnt = nullptr;
     // down GEMM (MFMA path): write `out` with the nontemporal hint.  For
     // outputs larger than the chip's last-level cache, which the combine reads
     // back once: their lines then go to HBM as they are written instead of

@@ -316,7 +316,7 @@ size_t MoeLayer::layout(int64_t cap, bool block, uint8_t* base, Workspace* w) co
     v.expert_count = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * Ecols_));
     v.expert_off = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * (Ecols_ + 1)));
     v.tiles = reinterpret_cast<TileInfo*>(take(sizeof(TileInfo) * mt));
-    v.tile_total = reinterpret_cast<int32_t*>(take(sizeof(int32_t)));
+    v.tile_total = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 3));  // + tail counters
     v.xperm = take(es * A * D_);
     v.h = take(es * A * H_);
     if (!dense_only_) v.yperm = take(es * A * D_);  // dense: the down GEMM writes y
@@ -548,6 +548,7 @@ int MoeLayer::run_routed(const void* x, void* y, int64_t rows, hipStream_t s,
     g1.a_cap = a_cap;
     g1.split_ws = w.split_ws;
     g1.split_cnt = w.split_cnt;
+    g1.tail_cnt = w.tile_total + 1;
     STAGE(mfma_ ? launch_gemm_gate_up_mfma(dt_, g1, s) : launch_gemm_gate_up_simt(dt_, g1, s),
           "gate/up GEMM");
     if ((rc = mark(4))) return rc;
@@ -557,6 +558,7 @@ int MoeLayer::run_routed(const void* x, void* y, int64_t rows, hipStream_t s,
     g2.W = d_w2_;
     g2.bias = d_b2_;
     g2.out = w.yperm;
+    g2.tail_cnt = w.tile_total + 2;
     g2.N = (int)D_;
     g2.K = (int)H_;
     g2.out_nt = rows * kslots_ * D_ * (int64_t)dtype_size(dt_) > kLastLevelCacheBytes;
@@ -631,6 +633,7 @@ int MoeLayer::forward_dense(const void* x, void* y, int64_t rows, hipStream_t s)
     g1.a_cap = mfma_ ? w.cap_rows : rows;
     g1.split_ws = w.split_ws;
     g1.split_cnt = w.split_cnt;
+    g1.tail_cnt = w.tile_total + 1;
     STAGE(mfma_ ? launch_gemm_gate_up_mfma(dt_, g1, s) : launch_gemm_gate_up_simt(dt_, g1, s),
           "gate/up GEMM");
     if ((rc = mark(4))) return rc;
@@ -640,6 +643,7 @@ int MoeLayer::forward_dense(const void* x, void* y, int64_t rows, hipStream_t s)
     g2.W = d_w2_;
     g2.bias = d_b2_;
     g2.out = y;  // rows stay in order: the output is y itself
+    g2.tail_cnt = w.tile_total + 2;
     g2.N = (int)D_;
     g2.K = (int)H_;
     STAGE(mfma_ ? launch_gemm_down_mfma(dt_, g2, s) : launch_gemm_down_simt(dt_, g2, s),

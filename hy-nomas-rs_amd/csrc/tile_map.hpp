@@ -73,32 +73,59 @@ struct WorkUnit {
     int slot;
 };
 
-// Work of block pid when `tiles` row tiles are live (tiles <= the max_tiles
-// the grid was sized for, grid = tile_grid(max_tiles, ntn) + kRound).  Whole
-// tiles come first in time order; the split units of the last r tiles come
-// last and fill the final round.  Returns false for blocks with no work.
-__host__ __device__ inline bool unit_coords(int pid, int ntn, int tiles, int turns, WorkUnit* u) {
+// The work units of `tiles` live row tiles in time order: the whole tiles,
+// then the split units of the last r tiles, which fill the final round.
+__host__ __device__ inline long long unit_count(int tiles, int ntn, int turns) {
     const long long T = (long long)tiles * ntn;
-    const long long L = time_order(pid);
     const int parts = split_parts(T, turns);
     const long long F = parts > 1 ? T - T % kRound : T;  // whole tiles
+    return F + (T - F) * parts;
+}
+
+// Unit L (0 <= L < unit_count) of that order.
+__host__ __device__ inline void unit_at(long long L, int ntn, int tiles, int turns, WorkUnit* u) {
+    const long long T = (long long)tiles * ntn;
+    const int parts = split_parts(T, turns);
+    const long long F = parts > 1 ? T - T % kRound : T;
     long long tile;
     if (L < F) {
         tile = L;
         u->part = 0;
         u->parts = 1;
         u->slot = -1;
-    } else if (L < F + (T - F) * parts) {
+    } else {
         const long long q = L - F;
         tile = F + q / parts;
         u->part = (int)(q % parts);
         u->parts = parts;
         u->slot = (int)(q / parts);
-    } else {
-        return false;
     }
     group_tile(tile, ntn, tiles, &u->mt, &u->nt);
+}
+
+// Work of block pid when `tiles` row tiles are live (tiles <= the max_tiles
+// the grid was sized for, grid = tile_grid(max_tiles, ntn) + kRound): unit
+// time_order(pid).  Returns false for blocks with no work.
+__host__ __device__ inline bool unit_coords(int pid, int ntn, int tiles, int turns, WorkUnit* u) {
+    const long long L = time_order(pid);
+    if (L >= unit_count(tiles, ntn, turns)) return false;
+    unit_at(L, ntn, tiles, turns, u);
     return true;
+}
+
+// The tail.  The XCDs do not run at the same speed (same work, same kernel:
+// the slowest finishes a few percent after the fastest), and with the static
+// map each XCD's share is fixed.  So the last kTailUnits units in time order
+// are handed out at run time instead: every block whose time-order index is
+// at or past tail_start (the grid's padding blocks included) takes a ticket
+// from a counter and runs unit tail_start + ticket, or nothing when the
+// tickets pass the last unit.  An XCD that is ahead reaches its tail blocks
+// sooner and takes more of the tail.  No block waits for another, and there
+// are at least as many such blocks as tail units (the grid has a round of
+// padding beyond the split units), so every unit runs exactly once.
+constexpr int kTailUnits = 2 * kRound;
+__host__ __device__ inline long long tail_start(long long units) {
+    return units > kTailUnits ? units - kTailUnits : 0;
 }
 
 }  // namespace nomas

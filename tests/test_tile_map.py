@@ -7,7 +7,8 @@ range, and every tile is named exactly once.  For the work units (whole
 tiles, plus the K-split parts of a short last round) every live tile is
 covered exactly once, or by exactly `parts` distinct parts that share one
 workspace slot; split units come after every whole tile in time order and
-fill at most one round.
+fill at most one round.  With the run-time tail (the last units handed out
+by ticket), every unit still runs exactly once and there are enough blocks.
 """
 import os
 import shutil
@@ -75,6 +76,31 @@ int main() {
             if (slot_of[t] >= 0) { if (slot_used[slot_of[t]]++) { printf("slot shared\n"); return 1; } }
           }
           if (first_split < (1LL << 60) && first_split < last_whole) { printf("split before whole\n"); return 1; }
+          // the run-time tail: blocks before tail_start run their own unit,
+          // every other block takes a ticket (tickets 0, 1, ... in any order);
+          // each unit must run exactly once
+          const long long W = nomas::unit_count(tiles, ntn, turns), Ws = nomas::tail_start(W);
+          if (Ws > W || W - Ws > nomas::kTailUnits) { printf("bad tail\n"); return 1; }
+          std::vector<int> runs(W, 0);
+          long long tail_blocks = 0;
+          for (long long pid = 0; pid < grid; ++pid) {
+            const long long L = nomas::time_order((int)pid);
+            if (L < Ws) {
+              nomas::WorkUnit a, b;
+              if (!nomas::unit_coords((int)pid, ntn, tiles, turns, &a)) { printf("static block idle\n"); return 1; }
+              nomas::unit_at(L, ntn, tiles, turns, &b);
+              if (a.mt != b.mt || a.nt != b.nt || a.part != b.part || a.parts != b.parts || a.slot != b.slot) {
+                printf("unit_at differs from unit_coords\n"); return 1;
+              }
+              runs[L]++;
+            } else {
+              ++tail_blocks;
+            }
+          }
+          if (tail_blocks < W - Ws) { printf("fewer tail blocks than tail units\n"); return 1; }
+          for (long long t = 0; t < tail_blocks && Ws + t < W; ++t) runs[Ws + t]++;
+          for (long long i = 0; i < W; ++i)
+            if (runs[i] != 1) { printf("unit %lld runs %d times (%d, %d, %d)\n", i, runs[i], tiles, ntn, turns); return 1; }
           ++units_checked;
         }
   printf("ok %ld %ld\n", pairs, units_checked);
