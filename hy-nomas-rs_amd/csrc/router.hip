@@ -123,14 +123,6 @@ __device__ __forceinline__ double quad_min(double v) {
     v = fmin(v, quad_dpp<0xB1>(v));
     return fmin(v, quad_dpp<0x4E>(v));
 }
-__device__ __forceinline__ float quad_maxf(float v) {
-    v = fmaxf(v, __int_as_float(quad_dpp<0xB1>(__float_as_int(v))));
-    return fmaxf(v, __int_as_float(quad_dpp<0x4E>(__float_as_int(v))));
-}
-__device__ __forceinline__ float quad_minf(float v) {
-    v = fminf(v, __int_as_float(quad_dpp<0xB1>(__float_as_int(v))));
-    return fminf(v, __int_as_float(quad_dpp<0x4E>(__float_as_int(v))));
-}
 // Reductions over a group of L = 4 or 8 consecutive lanes: the quad steps,
 // then for 8 lanes one exchange with the other quad of the 8 (row_half_mirror:
 // lane i and lane 7 - i).  Every lane of a quad holds the quad's value by
@@ -155,16 +147,19 @@ __device__ __forceinline__ double grp_sum(double v) {
     if constexpr (L == 8) v += quad_dpp<kHalfMirror>(v);
     return v;
 }
+
 template <int L>
-__device__ __forceinline__ float grp_maxf(float v) {
-    v = quad_maxf(v);
-    if constexpr (L == 8) v = fmaxf(v, __int_as_float(quad_dpp<kHalfMirror>(__float_as_int(v))));
+__device__ __forceinline__ uint32_t grp_maxu(uint32_t v) {
+    v = max(v, (uint32_t)quad_dpp<0xB1>((int)v));
+    v = max(v, (uint32_t)quad_dpp<0x4E>((int)v));
+    if constexpr (L == 8) v = max(v, (uint32_t)quad_dpp<kHalfMirror>((int)v));
     return v;
 }
 template <int L>
-__device__ __forceinline__ float grp_minf(float v) {
-    v = quad_minf(v);
-    if constexpr (L == 8) v = fminf(v, __int_as_float(quad_dpp<kHalfMirror>(__float_as_int(v))));
+__device__ __forceinline__ uint32_t grp_minu(uint32_t v) {
+    v = min(v, (uint32_t)quad_dpp<0xB1>((int)v));
+    v = min(v, (uint32_t)quad_dpp<0x4E>((int)v));
+    if constexpr (L == 8) v = min(v, (uint32_t)quad_dpp<kHalfMirror>((int)v));
     return v;
 }
 
@@ -179,53 +174,86 @@ __device__ __forceinline__ void grp_argmax(double& bv, int& bi) {
     step(quad_dpp<0x4E>(bv), quad_dpp<0x4E>(bi));
     if constexpr (L == 8) step(quad_dpp<kHalfMirror>(bv), quad_dpp<kHalfMirror>(bi));
 }
-template <int L>
-__device__ __forceinline__ void grp_argmaxf(float& bv, int& bi) {
-    auto step = [&](float ov, int oi) {
-        if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
-    };
-    step(__int_as_float(quad_dpp<0xB1>(__float_as_int(bv))), quad_dpp<0xB1>(bi));
-    step(__int_as_float(quad_dpp<0x4E>(__float_as_int(bv))), quad_dpp<0x4E>(bi));
-    if constexpr (L == 8)
-        step(__int_as_float(quad_dpp<kHalfMirror>(__float_as_int(bv))), quad_dpp<kHalfMirror>(bi));
-}
 
 // k rounds of argmax over a row held by a group of L lanes (lane sub: experts sub + L j,
-// bit j of `valid` set where that expert exists), the first maximum winning
-// (the lowest index among equal values); on the logits rounded to f32
-// (f32 = true) or on the f64 logits.  Returns this lane's chosen experts as
-// bits j.
+// bit j of `valid` set where that expert exists) on the f64 logits, the first
+// maximum winning (the lowest index among equal values).  Returns this lane's
+// chosen experts as bits j.
 template <int PL, int L>
 __device__ __forceinline__ uint32_t argmax_rounds(const double (&lv)[PL], uint32_t valid, int k,
-                                                  int sub, bool f32) {
+                                                  int sub) {
     uint32_t mine = 0;
-    if (f32) {
-        float lf[PL];
+    for (int it = 0; it < k; ++it) {
+        const uint32_t open = valid & ~mine;
+        double bv = 0.0;
+        int bi = -1;
 #pragma unroll
-        for (int j = 0; j < PL; ++j) lf[j] = (float)lv[j];
-        for (int it = 0; it < k; ++it) {
-            const uint32_t open = valid & ~mine;
-            float bv = 0.0f;
-            int bi = -1;
-#pragma unroll
-            for (int j = 0; j < PL; ++j)  // ascending expert: the first maximum stays
-                if (((open >> j) & 1u) && (bi < 0 || lf[j] > bv)) { bv = lf[j]; bi = sub + j * L; }
-            grp_argmaxf<L>(bv, bi);
-            if (bi >= 0 && bi % L == sub) mine |= 1u << (bi / L);
-        }
-    } else {
-        for (int it = 0; it < k; ++it) {
-            const uint32_t open = valid & ~mine;
-            double bv = 0.0;
-            int bi = -1;
-#pragma unroll
-            for (int j = 0; j < PL; ++j)
-                if (((open >> j) & 1u) && (bi < 0 || lv[j] > bv)) { bv = lv[j]; bi = sub + j * L; }
-            grp_argmax<L>(bv, bi);
-            if (bi >= 0 && bi % L == sub) mine |= 1u << (bi / L);
-        }
+        for (int j = 0; j < PL; ++j)
+            if (((open >> j) & 1u) && (bi < 0 || lv[j] > bv)) { bv = lv[j]; bi = sub + j * L; }
+        grp_argmax<L>(bv, bi);
+        if (bi >= 0 && bi % L == sub) mine |= 1u << (bi / L);
     }
     return mine;
+}
+
+// The same choice (up to 64 experts) on one 32-bit key per candidate: the
+// logit rounded to f32, its bits made to order as unsigned integers, the low
+// 6 bits replaced by 63 - expert.  A larger key is a larger value, or of
+// values equal to 17 significant bits ("truncated") the lower expert; a round
+// is a max over the lane's keys and the group's, and the winner's key is
+// cleared.  f64 -> f32 rounding and the truncation keep the order of unequal
+// values (not strictly), so with T the smallest truncated value chosen, every
+// candidate above T is in the f64 choice and every one below T is not.  Those
+// equal to T (when one of them was left out) are settled on their f64
+// logits: argmax_rounds over just them for the places left.
+template <int L>
+__device__ __forceinline__ int grp_sumi(int v) {
+    v += quad_dpp<0xB1>(v);
+    v += quad_dpp<0x4E>(v);
+    if constexpr (L == 8) v += quad_dpp<kHalfMirror>(v);
+    return v;
+}
+template <int PL, int L>
+__device__ __forceinline__ uint32_t argmax_keys(const double (&lv)[PL], uint32_t valid, int k,
+                                                int sub) {
+    uint32_t key[PL], trunc[PL];
+#pragma unroll
+    for (int j = 0; j < PL; ++j) {
+        const uint32_t b = __float_as_uint((float)lv[j]);
+        const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+        key[j] = (valid >> j) & 1u ? (o & ~63u) | (uint32_t)(63 - (sub + j * L)) : 0u;
+        trunc[j] = o >> 6;
+    }
+    // (keys are distinct, so each round clears one; with at least k experts
+    // a round's maximum is never 0)
+    for (int it = 0; it < k; ++it) {
+        uint32_t m = 0;
+#pragma unroll
+        for (int j = 0; j < PL; ++j) m = max(m, key[j]);
+        m = grp_maxu<L>(m);
+#pragma unroll
+        for (int j = 0; j < PL; ++j) key[j] = key[j] == m ? 0u : key[j];
+    }
+    uint32_t mine = 0;  // the valid experts whose keys were cleared
+#pragma unroll
+    for (int j = 0; j < PL; ++j) mine |= (key[j] == 0 ? 1u : 0u) << j;
+    mine &= valid;
+    uint32_t kth = ~0u, un = 0;
+#pragma unroll
+    for (int j = 0; j < PL; ++j) {
+        if ((mine >> j) & 1u) kth = min(kth, trunc[j]);
+        else if ((valid >> j) & 1u) un = max(un, trunc[j]);
+    }
+    kth = grp_minu<L>(kth);
+    if (kth > grp_maxu<L>(un)) return mine;  // (uniform over the group)
+    uint32_t sure = 0, tied = 0;
+#pragma unroll
+    for (int j = 0; j < PL; ++j) {
+        sure |= (((mine >> j) & 1u) && trunc[j] > kth ? 1u : 0u) << j;
+        tied |= (((valid >> j) & 1u) && trunc[j] == kth ? 1u : 0u) << j;
+    }
+    const int left = k - grp_sumi<L>(__popc(sure));
+    return sure | argmax_rounds<PL, L>(lv, tied, left, sub);
 }
 
 // OR of a 64-bit mask over a group of L lanes.
@@ -304,22 +332,10 @@ __device__ __forceinline__ void select_chunk(const double* s_logit, int* s_cnt, 
                 s += (double)pe[j];
             }
             s = grp_sum<L>(s);
-            // k rounds of argmax on the logits rounded to f32 (cheaper compares
-            // and half the registers).  f32 rounding is monotonic, so when the
-            // k-th chosen f32 value exceeds the best unchosen one strictly, the
-            // chosen set is the f64 one; otherwise (values within about 1e-7
-            // relative of each other) the rounds run again on the f64 logits.
-            uint32_t mine = argmax_rounds<PL, L>(lv, valid, k, sub, true);  // bit j: chosen
-            float kth32 = INFINITY, un32 = -INFINITY;
-#pragma unroll
-            for (int j = 0; j < PL; ++j) {
-                const float f = (float)lv[j];
-                if ((mine >> j) & 1u) kth32 = fminf(kth32, f);
-                else if ((valid >> j) & 1u) un32 = fmaxf(un32, f);
-            }
-            kth32 = grp_minf<L>(kth32);
-            un32 = grp_maxf<L>(un32);
-            if (!(kth32 > un32)) mine = argmax_rounds<PL, L>(lv, valid, k, sub, false);
+            // k rounds of argmax on 32-bit keys of the logits; where the k-th
+            // and best unchosen logits are within the keys' resolution (about
+            // 8e-6 relative), the f64 logits settle the candidates in between
+            const uint32_t mine = argmax_keys<PL, L>(lv, valid, k, sub);  // bit j: chosen
             const double inv_s = 1.0 / s;
             double kth = INFINITY, best_un = -INFINITY, psel = 0.0;
             uint64_t sel = 0;  // the row's chosen experts (after the OR over the quad)
