@@ -153,6 +153,45 @@ def test_exact_ties_go_to_the_lowest_index(E):
     assert not (sel[:, 2] & ~sel[:, 1]).any() and not (sel[:, E - 1] & ~sel[:, 1]).any()
 
 
+@pytest.mark.parametrize("E,k", [(8, 2), (40, 3), (64, 8)])
+def test_near_ties_inside_the_selection_keys(E, k):
+    # Twin router rows that differ only in one coordinate, by 2^-17, on a
+    # column of x set to +-1: the twins' f64 logits differ by 2^-17 (7.6e-6),
+    # far above the kernel's logit error (about 1e-8) and the 1e-6 near-tie
+    # exemption, but inside the resolution of the selection's 32-bit keys
+    # (17 significant bits: 1.5e-5 at these logit magnitudes of 2-4).  So
+    # the f64 logits, not the expert index, must decide between twins, and
+    # the indices must equal the oracle's on every row.
+    D, H, rows = 256, 128, 400
+    t, x = small_case(rows, D, E, k, H, 71 + E, router_std=0.2)
+    wr = t[PATH + ".router.weight"]
+    m0 = 5
+    x[:, m0] = np.where(np.arange(rows) % 2 == 0, 1.0, -1.0)
+    pairs = [(1, 2), (0, E - 1), (E // 2, E // 2 + 1)]
+    for a, b in pairs:
+        wr[b] = wr[a]
+        wr[a, m0] = 0.0
+        wr[b, m0] = 2.0 ** -17
+    layer = layer_from_tensors(t, "bf16", D, H, E, k)
+    rt, rx = rounded(t, x, "bf16")
+    p, _ = nm.workloads.oracle_params(rt, E)
+    layer.forward(to_device(x, "bf16"))
+    torch.cuda.synchronize()
+    idx, _, counts, _ = layer.routing(rows)
+    o_idx, _, o_logits, o_gap = O.route(rx, p["wr"], k)
+    for a, b in pairs:
+        assert np.allclose(np.abs(o_logits[:, b] - o_logits[:, a]), 2.0 ** -17, rtol=1e-6, atol=0)
+    sel = np.zeros((rows, E), bool)
+    np.put_along_axis(sel, o_idx.astype(np.int64), True, axis=1)
+    split = np.zeros(rows, bool)  # rows where the oracle chose exactly one twin
+    for a, b in pairs:
+        split |= sel[:, a] != sel[:, b]
+    assert split.sum() >= 10, "too few rows with a twin on each side of the k-th place"
+    assert (o_gap[split] >= 1e-6).all()  # none of them exempt
+    assert np.array_equal(idx, o_idx)
+    assert np.array_equal(counts, np.bincount(o_idx.ravel(), minlength=E))
+
+
 @pytest.mark.parametrize("E,k,dtype", [(16, 2, "bf16"), (24, 3, "bf16"), (32, 4, "f16"),
                                        (48, 6, "bf16"), (64, 8, "f16"), (65, 8, "bf16")])
 def test_router_pass_widths(E, k, dtype):
