@@ -26,6 +26,16 @@ __device__ __forceinline__ void lds_dma16(const void* sbase, uint32_t voff, uint
                  : "v"(voff), "s"(sbase), "s"(lds_base)
                  : "memory", "m0");
 }
+// The same through a raw buffer resource (buffer_load_dwordx4 ... lds): lanes
+// whose byte offset is at or past the resource's num_records fail the range
+// check, read no memory and return zeros.
+__device__ __forceinline__ void lds_dma16_buf(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff,
+                                              uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :
+                 : "v"(voff), "s"(rsrc), "s"(lds_base)
+                 : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // The LDS byte address of a __shared__ object (for M0).
