@@ -53,14 +53,20 @@ __device__ __forceinline__ void store16_nt(void* p, const uint4& v) {
     __builtin_nontemporal_store(t, reinterpret_cast<u32x4*>(p));
 }
 
+// 16 bytes of T from f32 values (rounded to T).
 template <typename T>
-__device__ __forceinline__ void store16(T* p, const float* in) {
+__device__ __forceinline__ uint4 pack16(const float* in) {
     Vec16<T> t;
 #pragma unroll
     for (int i = 0; i < Vec16<T>::N; ++i) t.v[i] = Elt<T>::from_f32(in[i]);
     uint4 raw;
     __builtin_memcpy(&raw, &t, 16);
-    *reinterpret_cast<uint4*>(p) = raw;
+    return raw;
+}
+
+template <typename T>
+__device__ __forceinline__ void store16(T* p, const float* in) {
+    *reinterpret_cast<uint4*>(p) = pack16<T>(in);
 }
 
 // One tile of token rows belonging to one expert: rows [row0, row0 + rows)

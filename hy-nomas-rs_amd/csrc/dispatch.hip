@@ -442,7 +442,9 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
                     acc[u][i] = seam_residual<T>(xv[u][i], Elt<T>::to_f32(Elt<T>::from_f32(acc[u][i])),
                                                  gv[u][i]);
             }
-            store16(out + row * a.D + (int64_t)c * EPC, acc[u]);
+            T* dst = out + row * a.D + (int64_t)c * EPC;
+            if (a.out_nt) store16_nt(dst, pack16<T>(acc[u]));
+            else store16(dst, acc[u]);
         }
     }
 }

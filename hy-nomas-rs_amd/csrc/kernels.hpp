@@ -154,6 +154,10 @@ struct CombineArgs {
     const void* resid_x;  // rows x D, model dtype
     const float* gate;    // sequences x D
     int64_t seq;
+    // write `out` with the nontemporal hint: when y_perm is larger than the
+    // last-level cache, its reads stream through it and would evict the
+    // output's dirty lines into the middle of them anyway
+    int out_nt = 0;
 };
 
 size_t router_lds_bytes(int E);

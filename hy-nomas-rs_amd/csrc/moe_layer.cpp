@@ -578,6 +578,7 @@ int MoeLayer::run_routed(const void* x, void* y, int64_t rows, hipStream_t s,
     ca.resid_x = blk ? x : nullptr;
     ca.gate = blk ? blk->gate : nullptr;
     ca.seq = blk ? blk->seq : 1;
+    ca.out_nt = g2.out_nt;
     STAGE(launch_combine(dt_, ca, s), "combine");
     if ((rc = mark(6))) return rc;
 #undef STAGE
