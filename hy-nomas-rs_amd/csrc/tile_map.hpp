@@ -115,17 +115,20 @@ __host__ __device__ inline bool unit_coords(int pid, int ntn, int tiles, int tur
 
 // The tail.  The XCDs do not run at the same speed (same work, same kernel:
 // the slowest finishes a few percent after the fastest), and with the static
-// map each XCD's share is fixed.  So the last kTailUnits units in time order
-// are handed out at run time instead: every block whose time-order index is
+// map each XCD's share is fixed.  So the last units in time order (at least
+// kTailUnits of them) are handed out at run time instead: every block whose time-order index is
 // at or past tail_start (the grid's padding blocks included) takes a ticket
 // from a counter and runs unit tail_start + ticket, or nothing when the
 // tickets pass the last unit.  An XCD that is ahead reaches its tail blocks
-// sooner and takes more of the tail.  No block waits for another, and there
-// are at least as many such blocks as tail units (the grid has a round of
-// padding beyond the split units), so every unit runs exactly once.
-constexpr int kTailUnits = 2 * kRound;
+// sooner and takes more of the tail.  The static part is whole rounds of all
+// XCDs, so every XCD has the same static work (otherwise an XCD with one more
+// static round reaches the tail after it has been handed out).  No block
+// waits for another, and there are at least as many such blocks as tail units
+// (the grid has a round of padding beyond the split units), so every unit
+// runs exactly once.
+constexpr int kTailUnits = 2 * kRound;  // at least; fewer than kTailUnits + kRound
 __host__ __device__ inline long long tail_start(long long units) {
-    return units > kTailUnits ? units - kTailUnits : 0;
+    return units > kTailUnits ? (units - kTailUnits) / kRound * kRound : 0;
 }
 
 }  // namespace nomas

@@ -80,7 +80,8 @@ int main() {
           // every other block takes a ticket (tickets 0, 1, ... in any order);
           // each unit must run exactly once
           const long long W = nomas::unit_count(tiles, ntn, turns), Ws = nomas::tail_start(W);
-          if (Ws > W || W - Ws > nomas::kTailUnits) { printf("bad tail\n"); return 1; }
+          if (Ws > W || Ws % nomas::kRound || W - Ws >= nomas::kTailUnits + nomas::kRound ||
+              (W > nomas::kTailUnits && W - Ws < nomas::kTailUnits)) { printf("bad tail\n"); return 1; }
           std::vector<int> runs(W, 0);
           long long tail_blocks = 0;
           for (long long pid = 0; pid < grid; ++pid) {
