@@ -351,17 +351,17 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
 // One wave per row: out[row] = sum_j w_j * y_perm[pos_j] over the row's slots
 // in ascending expert order (then the dense slot), accumulated in f32.  The
 // row's positions and gates are read once (lane j holds slot j) and broadcast
-// with readlane; each lane has up to 8 slots' loads of its chunks in flight
-// together.  kResid: the block's gated residual out = x + y * gate
+// with readlane; each lane has a group of slots' loads of its chunks in
+// flight together (8 slots of 2 chunks, or 4 of 6).  kResid: the block's gated residual out = x + y * gate
 // (block.rs:101), its x and gate loaded with the first slots' loads.  kNt:
-// nontemporal output stores.
-template <typename T, bool kResid, bool kNt>
+// nontemporal output stores.  kBatch: 16-byte chunks per lane per pass (6: a
+// whole 3072-wide 16-bit row per pass, its slots' loads 4 at a time).
+template <typename T, bool kResid, bool kNt, int kBatch>
 __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + wave;
     if (row >= a.rows) return;
     constexpr int EPC = 16 / sizeof(T);
-    constexpr int kBatch = 2;  // chunks per lane in flight
     const int nchunk = a.D / EPC;
     const int k = a.k_slots;   // slots past 64 are read from memory
     const T* __restrict__ y = static_cast<const T*>(a.y_perm);
@@ -424,7 +424,8 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
         using Lanes = std::true_type;
         const int k1 = min(k, kWave);
         int j0 = 0;
-        for (; j0 + 8 <= k1; j0 += 8) slots(std::integral_constant<int, 8>{}, Lanes{}, j0);
+        constexpr int kGroup = kBatch > 2 ? 4 : 8;  // slots per group: kGroup * kBatch loads
+        for (; j0 + kGroup <= k1; j0 += kGroup) slots(std::integral_constant<int, kGroup>{}, Lanes{}, j0);
         for (; j0 + 4 <= k1; j0 += 4) slots(std::integral_constant<int, 4>{}, Lanes{}, j0);
         switch (k1 - j0) {
             case 3: slots(std::integral_constant<int, 3>{}, Lanes{}, j0); break;
@@ -513,10 +514,16 @@ hipError_t launch_dispatch_t(const DispatchArgs& a, hipStream_t s) {
 template <typename T>
 hipError_t launch_combine_t(const CombineArgs& a, hipStream_t s) {
     const int nblk = (int)((a.rows + 3) / 4);
-    // the residual and the store kind as compile-time choices: a run-time
-    // store-kind test inside the chunk loop measured 3% slower
-    auto kern = a.gate ? (a.out_nt ? combine_kernel<T, true, true> : combine_kernel<T, true, false>)
-                       : (a.out_nt ? combine_kernel<T, false, true> : combine_kernel<T, false, false>);
+    // the residual, the store kind and the pass width as compile-time
+    // choices: a run-time store-kind test inside the chunk loop measured 3%
+    // slower.  Where the output goes out nontemporally (y_perm exceeds the
+    // last-level cache), whole rows per pass: each pass then writes a row's
+    // bytes at once (64 experts top-8: 182-184 -> 176-178 us; two chunks per
+    // pass measured the same as whole rows at top-2 with cached stores).
+    const bool whole = a.out_nt && (a.D / (16 / (int)sizeof(T))) % (kWave * 6) == 0;
+    auto kern = a.gate ? (a.out_nt ? combine_kernel<T, true, true, 2> : combine_kernel<T, true, false, 2>)
+              : a.out_nt ? (whole ? combine_kernel<T, false, true, 6> : combine_kernel<T, false, true, 2>)
+                         : combine_kernel<T, false, false, 2>;
     launch_kernel(kern, dim3(nblk), dim3(256), 0, s, a);
     return hipGetLastError();
 }
