@@ -520,7 +520,8 @@ hipError_t launch_combine_t(const CombineArgs& a, hipStream_t s) {
     // last-level cache), whole rows per pass: each pass then writes a row's
     // bytes at once (64 experts top-8: 182-184 -> 176-178 us; two chunks per
     // pass measured the same as whole rows at top-2 with cached stores).
-    const bool whole = a.out_nt && (a.D / (16 / (int)sizeof(T))) % (kWave * 6) == 0;
+    // 16-bit types only, where it was measured.
+    const bool whole = sizeof(T) == 2 && a.out_nt && (a.D / (16 / (int)sizeof(T))) % (kWave * 6) == 0;
     auto kern = a.gate ? (a.out_nt ? combine_kernel<T, true, true, 2> : combine_kernel<T, true, false, 2>)
               : a.out_nt ? (whole ? combine_kernel<T, false, true, 6> : combine_kernel<T, false, true, 2>)
                          : combine_kernel<T, false, false, 2>;

@@ -241,6 +241,16 @@ def test_shared_dense_branch(dtype):
     run_case(180, D, 6, 2, H, dtype, seed=27, s=0.6)
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_nontemporal_output_whole_row_combine(dtype):
+    """y_perm past the 256 MiB last-level cache (11,008 rows x top-4 x 3072 x 2 bytes = 270.5 MB):
+    the down GEMM and the combine store nontemporally, and the combine covers a whole 3072-wide
+    row per pass.  Checked on every 43rd row and the last."""
+    rows = 11008
+    sel = np.unique(np.r_[np.arange(0, rows, 43), rows - 1])
+    run_case(rows, 3072, 8, 4, 128, dtype, seed=29, check_rows=sel)
+
+
 def test_workspace_regrowth_and_determinism():
     E, D, H, k = 8, 256, 256, 2
     t, x = small_case(1500, D, E, k, H, 28)
