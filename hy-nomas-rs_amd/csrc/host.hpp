@@ -216,6 +216,7 @@ public:
     };
     int forward_block(const void* x, void* out, int64_t rows, const BlockArgs& b, hipStream_t s);
     int forward_host(const void* x, void* y, int64_t rows);
+    int forward_host_pieces(const void* x, void* y, int64_t rows, int np, void* dx, void* dy);
     int routing(int32_t* idx, float* w, int32_t* counts, float* gap);
     int set_profiling(bool on);
     int stage_times(float* ms6);
@@ -272,6 +273,19 @@ private:
     void* d_hio_ = nullptr;
     size_t hio_bytes_ = 0;  // bytes of each of the two halves
     HostStager stager_;
+    // large host-tensor forwards run in row pieces: the copies of one piece
+    // overlap the forward of another (two non-blocking streams of the
+    // default priority, an input-landed and a forward-done event per piece)
+    static constexpr int kHostMaxPieces = 4;
+    static constexpr int64_t kHostPieceRows = 4096;  // at least, per piece
+    hipStream_t hs_copy_ = nullptr, hs_comp_ = nullptr;
+    hipEvent_t hev_in_[kHostMaxPieces] = {}, hev_fw_[kHostMaxPieces] = {};
+    int host_pipe_setup();
+    // the routing of a pieced forward, gathered per piece: idx and w
+    // [rows][k_slots], gap [rows], then each piece's expert counts [E_cols]
+    void* d_route_ = nullptr;
+    size_t route_bytes_ = 0;
+    int host_pieces_ = 0;  // pieces of the last forward when it was pieced, else 0
 
     int64_t last_rows_ = -1;
     hipStream_t last_stream_ = nullptr;

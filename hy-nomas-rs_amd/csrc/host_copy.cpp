@@ -145,7 +145,9 @@ int HostStager::to_device(void* dst, const void* src, size_t bytes, hipStream_t 
     for (size_t off = 0; off < bytes; off += kChunk, ++c) {
         const size_t n = std::min(kChunk, bytes - off);
         const int b = c & 1;
-        if (c >= 2) STAGE_TRY(hipEventSynchronize(ev_[b]), "hipEventSynchronize");  // buffer b drained
+        // buffer b drained (its last DMA may belong to an earlier call: the
+        // pieces of a host forward stage one after another)
+        STAGE_TRY(hipEventSynchronize(ev_[b]), "hipEventSynchronize");
         pool_->copy(pin_[b], in + off, n);
         STAGE_TRY(hipMemcpyAsync(out + off, pin_[b], n, hipMemcpyHostToDevice, s), "hipMemcpyAsync H2D");
         STAGE_TRY(hipEventRecord(ev_[b], s), "hipEventRecord");

@@ -122,9 +122,17 @@ MoeLayer::MoeLayer(DenseTag, int64_t dim, int64_t hidden, DType dt, int device)
 MoeLayer::~MoeLayer() {
     DeviceGuard g(device_);
     free_workspace();
-    for (void* p : {d_wr_, d_w1_, (void*)d_b1_, d_w2_, (void*)d_b2_, d_hio_})
+    if (hs_copy_) (void)hipStreamSynchronize(hs_copy_);
+    if (hs_comp_) (void)hipStreamSynchronize(hs_comp_);
+    for (void* p : {d_wr_, d_w1_, (void*)d_b1_, d_w2_, (void*)d_b2_, d_hio_, d_route_})
         if (p) (void)hipFree(p);
     for (hipEvent_t e : events_) (void)hipEventDestroy(e);
+    for (int i = 0; i < kHostMaxPieces; ++i) {
+        if (hev_in_[i]) (void)hipEventDestroy(hev_in_[i]);
+        if (hev_fw_[i]) (void)hipEventDestroy(hev_fw_[i]);
+    }
+    for (hipStream_t s : {hs_copy_, hs_comp_})
+        if (s) (void)hipStreamDestroy(s);
     if (done_) (void)hipEventDestroy(done_);
 }
 
@@ -445,6 +453,7 @@ int MoeLayer::finish_forward(int64_t rows, hipStream_t s, const Workspace& w) {
     // done_ is created with the weights; recording it allocates nothing
     HIP_TRY(hipEventRecord(done_, s));
     done_recorded_ = true;
+    host_pieces_ = 0;  // routing() reads this forward's workspace
     last_rows_ = rows;
     last_stream_ = s;
     last_ws_ = w;
@@ -675,10 +684,106 @@ int MoeLayer::forward_host(const void* x, void* y, int64_t rows) {
     }
     void* dx = d_hio_;
     void* dy = static_cast<uint8_t*>(d_hio_) + hio_bytes_;
-    int rc = stager_.to_device(dx, x, bytes, nullptr);
-    if (rc == NOMAS_OK) rc = forward(dx, dy, rows, nullptr);
-    if (rc == NOMAS_OK) rc = stager_.to_host(y, dy, bytes, nullptr);
-    return rc;
+    const int np = rows >= 2 * kHostPieceRows
+                       ? (int)std::min<int64_t>(kHostMaxPieces, rows / kHostPieceRows)
+                       : 1;
+    if (np == 1) {
+        host_pieces_ = 0;
+        int rc = stager_.to_device(dx, x, bytes, nullptr);
+        if (rc == NOMAS_OK) rc = forward(dx, dy, rows, nullptr);
+        if (rc == NOMAS_OK) rc = stager_.to_host(y, dy, bytes, nullptr);
+        return rc;
+    }
+    return forward_host_pieces(x, y, rows, np, dx, dy);
+}
+
+int MoeLayer::host_pipe_setup() {
+    if (hs_comp_) return NOMAS_OK;
+    for (hipStream_t* s : {&hs_copy_, &hs_comp_})
+        if (!*s) HIP_TRY(hipStreamCreateWithFlags(s, hipStreamNonBlocking));
+    for (int i = 0; i < kHostMaxPieces; ++i) {
+        if (!hev_in_[i]) HIP_TRY(hipEventCreateWithFlags(&hev_in_[i], hipEventDisableTiming));
+        if (!hev_fw_[i]) HIP_TRY(hipEventCreateWithFlags(&hev_fw_[i], hipEventDisableTiming));
+    }
+    return NOMAS_OK;
+}
+
+// A large host-tensor forward in np row pieces (whole multiples of 64 rows,
+// the last one shorter): every piece's input is copied in first, each on the
+// copy stream, and the compute stream runs piece p's forward once its input
+// has landed; then every piece's output is copied out once its forward is
+// done.  The host thread stages piece p + 1 in while the GPU computes piece
+// p, and piece p out while it computes p + 1.  Each piece is an ordinary
+// forward: rows are independent, so the results are those of a forward over
+// the piece's rows (a K-split GEMM tile can round differently than in one
+// forward over all rows, within the same bars).  The routing of every piece
+// is kept, so routing() reads the whole call back.
+int MoeLayer::forward_host_pieces(const void* x, void* y, int64_t rows, int np, void* dx, void* dy) {
+    int rc = host_pipe_setup();
+    if (rc != NOMAS_OK) return rc;
+    const size_t rb = (size_t)D_ * dtype_size(dt_);  // bytes per row
+    const int64_t per = ((rows + np - 1) / np + kRouterRows - 1) / kRouterRows * kRouterRows;
+    const size_t route = dense_only_ ? 0 : (size_t)rows * kslots_ * 8 + (size_t)rows * 4 +
+                                               (size_t)np * Ecols_ * 4;
+    if (route > route_bytes_) {
+        if (hs_comp_) HIP_TRY(hipStreamSynchronize(hs_comp_));
+        if (d_route_) HIP_TRY(hipFree(d_route_));
+        d_route_ = nullptr;
+        route_bytes_ = 0;
+        HIP_TRY(hipMalloc(&d_route_, route));
+        route_bytes_ = route;
+    }
+    int32_t* r_idx = static_cast<int32_t*>(d_route_);
+    float* r_w = reinterpret_cast<float*>(r_idx + rows * kslots_);
+    float* r_gap = r_w + rows * kslots_;
+    int32_t* r_cnt = reinterpret_cast<int32_t*>(r_gap + rows);
+    auto fail = [&](int code) {  // nothing in flight outlives the call
+        (void)hipStreamSynchronize(hs_copy_);
+        (void)hipStreamSynchronize(hs_comp_);
+        host_pieces_ = 0;
+        return code;
+    };
+    int n_pieces = 0;
+    for (int p = 0; p < np; ++p) {
+        const int64_t off = p * per, n = std::min(per, rows - off);
+        if (n <= 0) break;
+        n_pieces = p + 1;
+        const size_t o = (size_t)off * rb;
+        rc = stager_.to_device(static_cast<uint8_t*>(dx) + o, static_cast<const uint8_t*>(x) + o,
+                               (size_t)n * rb, hs_copy_);
+        if (rc != NOMAS_OK) return fail(rc);
+        if (hipEventRecord(hev_in_[p], hs_copy_) != hipSuccess ||
+            hipStreamWaitEvent(hs_comp_, hev_in_[p], 0) != hipSuccess)
+            return fail(set_error(NOMAS_ERR_HIP, "host piece %d: event failed", p));
+        rc = forward(static_cast<uint8_t*>(dx) + o, static_cast<uint8_t*>(dy) + o, n, hs_comp_);
+        if (rc != NOMAS_OK) return fail(rc);
+        if (!dense_only_) {
+            const Workspace& w = last_ws_;
+            const hipMemcpyKind d2d = hipMemcpyDeviceToDevice;
+            if (hipMemcpyAsync(r_idx + off * kslots_, w.idx, sizeof(int32_t) * n * kslots_, d2d, hs_comp_) ||
+                hipMemcpyAsync(r_w + off * kslots_, w.w, sizeof(float) * n * kslots_, d2d, hs_comp_) ||
+                hipMemcpyAsync(r_gap + off, w.gap, sizeof(float) * n, d2d, hs_comp_) ||
+                hipMemcpyAsync(r_cnt + (int64_t)p * Ecols_, w.expert_count, sizeof(int32_t) * Ecols_, d2d,
+                               hs_comp_))
+                return fail(set_error(NOMAS_ERR_HIP, "host piece %d: routing copy failed", p));
+        }
+        if (hipEventRecord(hev_fw_[p], hs_comp_) != hipSuccess)
+            return fail(set_error(NOMAS_ERR_HIP, "host piece %d: event failed", p));
+    }
+    for (int p = 0; p < n_pieces; ++p) {
+        const int64_t off = p * per, n = std::min(per, rows - off);
+        const size_t o = (size_t)off * rb;
+        if (hipStreamWaitEvent(hs_copy_, hev_fw_[p], 0) != hipSuccess)
+            return fail(set_error(NOMAS_ERR_HIP, "host piece %d: event failed", p));
+        rc = stager_.to_host(static_cast<uint8_t*>(y) + o, static_cast<const uint8_t*>(dy) + o,
+                             (size_t)n * rb, hs_copy_);
+        if (rc != NOMAS_OK) return fail(rc);
+    }
+    // the copy-out of the last piece has finished on the host; the routing
+    // copies are ordered before the events it waited for
+    host_pieces_ = n_pieces;
+    last_rows_ = rows;
+    return NOMAS_OK;
 }
 
 int MoeLayer::routing(int32_t* idx, float* w, int32_t* counts, float* gap) {
@@ -691,19 +796,40 @@ int MoeLayer::routing(int32_t* idx, float* w, int32_t* counts, float* gap) {
         if (counts) std::memset(counts, 0, sizeof(int32_t) * E_);
         return NOMAS_OK;
     }
+    // a pieced host-tensor forward keeps its routing in d_route_
+    const int32_t* s_idx = last_ws_.idx;
+    const float* s_w = last_ws_.w;
+    const float* s_gap = last_ws_.gap;
+    if (host_pieces_ > 0) {
+        s_idx = static_cast<const int32_t*>(d_route_);
+        s_w = reinterpret_cast<const float*>(s_idx + rows * kslots_);
+        s_gap = s_w + rows * kslots_;
+    }
     if (idx || w) {
         std::vector<int32_t> hi((size_t)(rows * kslots_));
         std::vector<float> hw((size_t)(rows * kslots_));
-        HIP_TRY(hipMemcpy(hi.data(), last_ws_.idx, hi.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
-        HIP_TRY(hipMemcpy(hw.data(), last_ws_.w, hw.size() * sizeof(float), hipMemcpyDeviceToHost));
+        HIP_TRY(hipMemcpy(hi.data(), s_idx, hi.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
+        HIP_TRY(hipMemcpy(hw.data(), s_w, hw.size() * sizeof(float), hipMemcpyDeviceToHost));
         for (int64_t r = 0; r < rows; ++r)
             for (int64_t j = 0; j < k_; ++j) {
                 if (idx) idx[r * k_ + j] = hi[(size_t)(r * kslots_ + j)];
                 if (w) w[r * k_ + j] = hw[(size_t)(r * kslots_ + j)];
             }
     }
-    if (counts) HIP_TRY(hipMemcpy(counts, last_ws_.expert_count, sizeof(int32_t) * E_, hipMemcpyDeviceToHost));
-    if (gap) HIP_TRY(hipMemcpy(gap, last_ws_.gap, sizeof(float) * rows, hipMemcpyDeviceToHost));
+    if (counts) {
+        if (host_pieces_ > 0) {  // the pieces' counts, added
+            std::vector<int32_t> pc((size_t)host_pieces_ * Ecols_);
+            HIP_TRY(hipMemcpy(pc.data(), s_gap + rows, pc.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
+            for (int64_t e = 0; e < E_; ++e) {
+                int64_t c = 0;
+                for (int p = 0; p < host_pieces_; ++p) c += pc[(size_t)p * Ecols_ + e];
+                counts[e] = (int32_t)c;
+            }
+        } else {
+            HIP_TRY(hipMemcpy(counts, last_ws_.expert_count, sizeof(int32_t) * E_, hipMemcpyDeviceToHost));
+        }
+    }
+    if (gap) HIP_TRY(hipMemcpy(gap, s_gap, sizeof(float) * rows, hipMemcpyDeviceToHost));
     return NOMAS_OK;
 }
 

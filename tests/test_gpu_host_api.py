@@ -66,6 +66,35 @@ def test_host_tensor_forward_in_several_staging_chunks():
     assert torch.equal(layer.forward(xd[:5].cpu()), yd[:5])
 
 
+def test_host_tensor_forward_in_pieces():
+    # 10,000 bf16 rows of 256 (the MFMA path): two pieces of 5,056 and 4,944 rows, the copies of one
+    # overlapping the other's forward.  The routing of the whole call is kept (the pieces are whole
+    # 64-row router chunks, so it equals a device forward's bit for bit); outputs against the oracle
+    # and the device forward (a K-split tile may round differently in a piece).
+    rows, D, E, k, H = 10_000, 256, 8, 2, 128
+    t, x = small_case(rows, D, E, k, H, 33)
+    layer = layer_from_tensors(t, "bf16", D, H, E, k)
+    rt, rx = rounded(t, x, "bf16")
+    p, _ = nm.workloads.oracle_params(rt, E)
+    xd = to_device(x, "bf16")
+    yd = layer.forward(xd).float().cpu().numpy()
+    d_route = layer.routing(rows)
+    yh = layer.forward(xd.cpu())  # pageable in and out, staged
+    assert yh.device.type == "cpu"
+    h_route = layer.routing(rows)
+    for a, b in zip(h_route, d_route):
+        assert np.array_equal(a, b)
+    got = yh.float().numpy()
+    sel = np.arange(0, rows, 37)
+    ref, _, _, _ = O.forward_sparse(rx, p, k, rows=sel)
+    assert rel_err(got[sel], ref) <= 2e-2
+    assert rel_err(got, yd) <= 1e-2  # at most a bf16 ulp where rounding differs
+    # pinned in and out: straight DMA, the same pieces, the same bits
+    yp = torch.empty_like(yh).pin_memory()
+    layer.forward(xd.cpu().pin_memory(), out=yp)
+    assert torch.equal(yp, yh)
+
+
 @pytest.mark.parametrize("src_dtype,model", [(np.float32, "bf16"), (np.float16, "f16"),
                                              (np.float32, "f32")])
 def test_safetensors_checkpoint_equals_in_memory_tensors(tmp_path, src_dtype, model):
