@@ -104,6 +104,22 @@ def test_host_tensors_and_leading_dims():
     assert torch.equal(yh.reshape(96, 256).float(), torch.from_numpy(got))
 
 
+def test_host_tensors_in_pieces():
+    # 9,000 host rows: two pieces of 4,544 and 4,456 rows whose copies overlap the other's forward;
+    # against the oracle and a device forward of all rows (a K-split tile may round differently)
+    t, x = ffn_case(9000, 256, 256, 46)
+    ffn = nm.FeedForward.from_source(nm.Weights.from_tensors(t, "bf16"), PATH, 256, 256)
+    raw = nm.to_model_dtype(x, "bf16")
+    xh = torch.from_numpy(raw.view(np.int16)).view(torch.bfloat16)
+    yd = ffn.forward(xh.cuda()).float().cpu().numpy()
+    yh = ffn.forward(xh)
+    assert not yh.is_cuda
+    got = yh.float().numpy()
+    ref = O.ffn(nm.widen(raw, "bf16"), oracle_f(t, "bf16"))
+    assert rel_err(got, ref) <= TOL["bf16"]
+    assert rel_err(got, yd) <= 1e-2  # at most a bf16 ulp where rounding differs
+
+
 def test_safetensors_checkpoint_equals_in_memory_tensors(tmp_path):
     t, x = ffn_case(80, 256, 256, seed=46)
     f = str(tmp_path / "ffn.safetensors")
