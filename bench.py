@@ -9,7 +9,7 @@ scan, dispatch, gate/up GEMM, down GEMM, combine) with x already resident in
 HBM.  Prints one JSON line.
 
   python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
-                  [--ffn | --block | --vendor-gemm | --hbm-yardstick]
+                  [--ffn | --block | --vendor-gemm | --hbm-yardstick | --host-tensors]
 """
 from __future__ import annotations
 
@@ -140,6 +140,50 @@ def bench_ffn(args, w) -> int:
         "stages_ms": st, "gemm_tflops": flops / (gemm_ms * 1e-3) / 1e12,
         "gemm_frac": flops / (gemm_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
         "uses_mfma": ffn.uses_mfma}))
+    return 0
+
+
+def bench_host_tensors(args, w) -> int:
+    """The host-tensor forward (nomas_moe_forward_host, the candle-CPU-tensor call): x in and y out
+    in host memory, PCIe copies included, with pageable and with pinned buffers, against the
+    device-resident forward.  Wall-clock per forward over the timed steps (each host-tensor call
+    returns with y in host memory)."""
+    import numpy as np
+    import torch
+    import nomas_moe as nm
+    from nomas_moe import workloads as wl
+
+    dt = nm.DataType.of(w.dtype)
+    layer = nm.MoeLayer.from_source(nm.Weights.from_tensors(wl.make_params(w), dt), wl.moe_path(),
+                                    w.dim, w.hidden, nm.MoeConfig(w.experts, w.top_k, 0.0, 0))
+    raw = nm.to_model_dtype(wl.make_x(w), dt)
+    xh = torch.from_numpy(raw.view(np.int16) if raw.dtype == np.uint16 else raw).view(dt.torch)
+    cases = {"pageable": (xh, torch.empty_like(xh)),
+             "pinned": (xh.pin_memory(), torch.empty_like(xh).pin_memory())}
+    xd = xh.cuda()
+    cases["device"] = (xd, torch.empty_like(xd))
+    ms = {}
+    for name, (x, y) in cases.items():
+        for _ in range(args.warmup):
+            layer.forward(x, out=y)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            layer.forward(x, out=y)
+        torch.cuda.synchronize()
+        ms[name] = (time.perf_counter() - t0) / args.steps * 1e3
+    mb = w.rows * w.dim * raw.itemsize / 1e6
+    print(json.dumps({
+        "metric": f"host-tensor MoE-FFN tokens/s at dim{w.dim} E{w.experts} top{w.top_k} {w.dtype}, "
+                  "PCIe copies included",
+        "value": w.rows / (ms["pageable"] * 1e-3), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms["pageable"],
+        "higher_is_better": True, "dtype": w.dtype, "data": "synthetic (seeded N(0,1) rows, "
+        "random-init weights of this shape)",
+        "config": {"workload": f"{w.name}: {w.note}", "rows": w.rows,
+                   "x_and_y_mb_each_way": round(mb, 1)},
+        "ms_per_forward": ms,
+        "tokens_per_s": {k: w.rows / (v * 1e-3) for k, v in ms.items()}}))
     return 0
 
 
@@ -333,6 +377,9 @@ def main() -> int:
     ap.add_argument("--hbm-yardstick", action="store_true",
                     help="time torch's own kernels on the dispatch's and combine's byte mix "
                          "(a yardstick for the memory-bound stages)")
+    ap.add_argument("--host-tensors", action="store_true",
+                    help="time the host-tensor forward (x and y in host memory, PCIe copies "
+                         "included; pageable and pinned) against the device-resident one")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only run a plain copy of this many MB (counter calibration) and exit")
     args = ap.parse_args()
@@ -357,6 +404,8 @@ def main() -> int:
         return bench_vendor_gemm(args, w)
     if args.hbm_yardstick:
         return bench_hbm_yardstick(args, w)
+    if args.host_tensors:
+        return bench_host_tensors(args, w)
     dt = nm.DataType.of(w.dtype)
     print(f"[bench] workload {w.name}: rows={w.rows} D={w.dim} E={w.experts} k={w.top_k} "
           f"H={w.hidden} {w.dtype}", file=sys.stderr, flush=True)
