@@ -53,6 +53,14 @@ __device__ __forceinline__ void store16_nt(void* p, const uint4& v) {
     __builtin_nontemporal_store(t, reinterpret_cast<u32x4*>(p));
 }
 
+// A 16-byte load with the nontemporal hint (global_load_dwordx4 ... nt), for
+// data read exactly once.
+__device__ __forceinline__ uint4 load16_nt(const void* p) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return uint4{t.x, t.y, t.z, t.w};
+}
+
 // 16 bytes of T from f32 values (rounded to T).
 template <typename T>
 __device__ __forceinline__ uint4 pack16(const float* in) {

@@ -406,9 +406,12 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
                 const int64_t pc = ok ? p[t] : 0;
                 w[t] = ok ? w[t] : 0.0f;
 #pragma unroll
-                for (int u = 0; u < kBatch; ++u)
-                    raw[t][u] = *reinterpret_cast<const uint4*>(
-                        y + pc * a.D + (int64_t)min(c0 + u * kWave, nchunk - 1) * EPC);
+                for (int u = 0; u < kBatch; ++u) {
+                    const T* src = y + pc * a.D + (int64_t)min(c0 + u * kWave, nchunk - 1) * EPC;
+                    // y_perm past the last-level cache is read once, nontemporally
+                    if constexpr (kNt) raw[t][u] = load16_nt(src);
+                    else raw[t][u] = *reinterpret_cast<const uint4*>(src);
+                }
             }
 #pragma unroll
             for (int t = 0; t < N; ++t) {
