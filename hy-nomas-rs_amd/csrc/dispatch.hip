@@ -62,8 +62,11 @@ __host__ __device__ inline bool dispatch_fits(int E_cols, int k) {
 //     slab 1 once step 1's values have arrived: steps 2-3 then wait on LDS
 //     only), so the bookkeeping overlaps the copy's first memory latencies.
 //     x_perm is written with the nontemporal hint: the GEMM reads it much
-//     later, from HBM.
-template <typename T, bool kKBlocked>
+//     later, from HBM.  Where x is larger than the L2 caches together, its
+//     rows are loaded with that hint too (no later kernel of the forward reads
+//     them); a smaller x is still in L2 from the router and loads faster
+//     without it.
+template <typename T, bool kKBlocked, bool kNtX>
 __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) {
     extern __shared__ __align__(16) unsigned char s_raw[];
     // parts > 1: blocks b * parts .. b * parts + parts - 1 share chunk b, each
@@ -99,7 +102,9 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
         const int q = tid + u * kProdThreads;
         const int r = min(q / kSlabPieces, nvalid - 1);
         const int c = min((sl0 + sl) * kSlabPieces + q % kSlabPieces, nck - 1);
-        return *reinterpret_cast<const uint4*>(x + (row0 + r) * (int64_t)a.D + (int64_t)c * EPC);
+        const T* src = x + (row0 + r) * (int64_t)a.D + (int64_t)c * EPC;
+        if constexpr (kNtX) return load16_nt(src);
+        else return *reinterpret_cast<const uint4*>(src);
     };
     // slab 0, in flight with step 1's loads
     uint4 f0, f1, f2, f3;
@@ -407,10 +412,9 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
                 w[t] = ok ? w[t] : 0.0f;
 #pragma unroll
                 for (int u = 0; u < kBatch; ++u) {
-                    const T* src = y + pc * a.D + (int64_t)min(c0 + u * kWave, nchunk - 1) * EPC;
-                    // y_perm past the last-level cache is read once, nontemporally
-                    if constexpr (kNt) raw[t][u] = load16_nt(src);
-                    else raw[t][u] = *reinterpret_cast<const uint4*>(src);
+                    // y_perm is read once: nontemporally, so that it does not
+                    // push other data (the next forward's x) out of the caches
+                    raw[t][u] = load16_nt(y + pc * a.D + (int64_t)min(c0 + u * kWave, nchunk - 1) * EPC);
                 }
             }
 #pragma unroll
@@ -500,8 +504,13 @@ hipError_t launch_dispatch_t(const DispatchArgs& a, hipStream_t s) {
         (a.kblocked && (int64_t)a.D * (int64_t)sizeof(T) % kKBlockBytes != 0))
         return hipErrorInvalidValue;
     const size_t lds = dispatch_lds(a.E_cols, a.k_slots);
-    // the x_perm layout as a compile-time choice: no layout test in the copy loop
-    auto kern = a.kblocked ? dispatch_kernel<T, true> : dispatch_kernel<T, false>;
+    // the x_perm layout and the load hint as compile-time choices: no tests in
+    // the copy loop.  Nontemporal x loads: headline 14,232 rows (87 MB)
+    // 41.9 -> 40.2 us; one 4,680-row segment (29 MB, in L2 after the router)
+    // 17.6 -> 19.5 us (A/B on one box, two repeats each).
+    const bool nt_x = a.rows * (int64_t)a.D * (int64_t)sizeof(T) > kL2TotalBytes;
+    auto kern = a.kblocked ? (nt_x ? dispatch_kernel<T, true, true> : dispatch_kernel<T, true, false>)
+                           : (nt_x ? dispatch_kernel<T, false, true> : dispatch_kernel<T, false, false>);
     hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                          (int)lds);
     if (err != hipSuccess) return err;

@@ -138,6 +138,8 @@ struct GemmArgs {
 };
 // MI355X's last-level cache (the Infinity Cache in front of HBM).
 constexpr int64_t kLastLevelCacheBytes = (int64_t)256 << 20;
+// MI355X's L2 caches together (8 XCDs x 4 MB).
+constexpr int64_t kL2TotalBytes = (int64_t)32 << 20;
 // One split unit's partial tile: 256 x 256 f32.
 constexpr int64_t kSplitUnitFloats = 256 * 256;
 constexpr int kSplitUnits = 256;
