@@ -154,11 +154,17 @@ struct Workspace {
     void* block_h = nullptr;         // forward_block: rows x D
 };
 
-// The device scratch array of the no-allocation forward (scratch.hip).
-constexpr size_t kScratchBytes = (size_t)256 << 20;
+// The device scratch array of the no-allocation forward (scratch.hip):
+// 512 MiB per GPU, enough for one 4,744-row segment of the 8B preset
+// (dim 3072, 8 experts, top-2, hidden 8192: 8,128 rows).
+constexpr size_t kScratchBytes = (size_t)512 << 20;
 // Its address on `device` (looked up once per device; the first call also
 // clears the split-tile counters with a kernel on `s`).  Never allocates.
-int scratch_acquire(int device, hipStream_t s, void** out);
+// Each call counts as one use of the array: *gen receives that use's number
+// on this device (1, 2, ...).
+int scratch_acquire(int device, hipStream_t s, void** out, uint64_t* gen);
+// The number of the last use of the array on `device` (0 before the first).
+uint64_t scratch_generation(int device);
 
 // Parameters of one Lin in f32, reference (out, in) layout.
 struct LinF32 {
@@ -267,6 +273,7 @@ private:
     Workspace ws_;
     // where the last forward's routing lives: ws_, or the scratch array
     Workspace last_ws_;
+    uint64_t last_scratch_gen_ = 0;  // scratch use of the last no-allocation forward
     bool last_in_scratch_ = false;
     // forward_host: device copies of x and y, kept between calls (grown as
     // needed), and the pinned staging of the copies

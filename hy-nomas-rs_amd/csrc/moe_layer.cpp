@@ -438,7 +438,8 @@ int MoeLayer::forward_noalloc(const void* x, void* y, int64_t rows, hipStream_t 
     DeviceGuard g(device_);
     if (!g.ok) return set_error(NOMAS_ERR_HIP, "hipSetDevice(%d) failed", device_);
     void* base = nullptr;
-    rc = scratch_acquire(device_, s, &base);
+    uint64_t gen = 0;
+    rc = scratch_acquire(device_, s, &base, &gen);
     if (rc != NOMAS_OK) return rc;
     Workspace w;
     layout(cap, false, static_cast<uint8_t*>(base), &w);
@@ -446,6 +447,7 @@ int MoeLayer::forward_noalloc(const void* x, void* y, int64_t rows, hipStream_t 
     rc = run_routed(x, y, rows, s, nullptr, w);
     if (rc != NOMAS_OK) return rc;
     last_in_scratch_ = true;
+    last_scratch_gen_ = gen;
     return finish_forward(rows, s, w);
 }
 
@@ -733,10 +735,16 @@ int MoeLayer::forward_host_pieces(const void* x, void* y, int64_t rows, int np, 
         HIP_TRY(hipMalloc(&d_route_, route));
         route_bytes_ = route;
     }
-    int32_t* r_idx = static_cast<int32_t*>(d_route_);
-    float* r_w = reinterpret_cast<float*>(r_idx + rows * kslots_);
-    float* r_gap = r_w + rows * kslots_;
-    int32_t* r_cnt = reinterpret_cast<int32_t*>(r_gap + rows);
+    // the pieces' routing (a dense feed-forward has none, and no d_route_)
+    int32_t* r_idx = nullptr;
+    float *r_w = nullptr, *r_gap = nullptr;
+    int32_t* r_cnt = nullptr;
+    if (!dense_only_) {
+        r_idx = static_cast<int32_t*>(d_route_);
+        r_w = reinterpret_cast<float*>(r_idx + rows * kslots_);
+        r_gap = r_w + rows * kslots_;
+        r_cnt = reinterpret_cast<int32_t*>(r_gap + rows);
+    }
     auto fail = [&](int code) {  // nothing in flight outlives the call
         (void)hipStreamSynchronize(hs_copy_);
         (void)hipStreamSynchronize(hs_comp_);
@@ -789,6 +797,10 @@ int MoeLayer::forward_host_pieces(const void* x, void* y, int64_t rows, int np, 
 int MoeLayer::routing(int32_t* idx, float* w, int32_t* counts, float* gap) {
     if (dense_only_) return set_error(NOMAS_ERR_STATE, "a dense feed-forward has no routing");
     if (last_rows_ < 0) return set_error(NOMAS_ERR_STATE, "no forward has run on this handle");
+    if (last_in_scratch_ && last_rows_ > 0 && scratch_generation(device_) != last_scratch_gen_)
+        return set_error(NOMAS_ERR_STATE,
+                         "the routing of this handle's last (no-allocation) forward was overwritten "
+                         "by a later no-allocation forward on device %d", device_);
     DeviceGuard g(device_);
     HIP_TRY(hipStreamSynchronize(last_stream_));
     const int64_t rows = last_rows_;

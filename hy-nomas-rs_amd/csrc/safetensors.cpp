@@ -1,6 +1,7 @@
-// Minimal safetensors reader for the MoE parameters (the format candle's
-// safetensors::load reads in weights.rs:113-116, through the `safetensors`
-// crate 0.7 pinned by nomas-core/Cargo.toml:11): an 8-byte little-endian
+// Minimal safetensors reader for the MoE parameters (the format
+// candle_core::safetensors::load reads in weights.rs:112-115, through the
+// `safetensors` crate 0.8.0 that candle-core 0.11.1 depends on, Cargo.lock:185
+// and :1293-1296): an 8-byte little-endian
 // header length, a JSON header mapping tensor names to
 // {"dtype", "shape", "data_offsets": [begin, end]}, then the payload.
 //
@@ -13,7 +14,10 @@
 // entirely indexed, and cannot contain holes").  Any violation is
 // NOMAS_ERR_IO with the message "loading <path>: <reason>", the form of
 // load_dit's error (weights.rs:112-115).  Only the requested tensors are
-// read from disk.
+// read from disk.  The JSON itself is held to what the crate's serde_json
+// parse accepts: strict JSON, `__metadata__` null or an object of strings, at
+// most 128 nested containers; the parser is iterative, so no header can
+// exhaust the stack.
 #include <sys/types.h>
 
 #include <algorithm>
@@ -34,7 +38,7 @@ struct Entry {
     int64_t begin = -1, end = -1;
 };
 
-// Tiny recursive-descent JSON parser covering the safetensors header.
+// Small JSON parser covering the safetensors header.
 class Json {
 public:
     explicit Json(const std::string& s) : s_(s) {}
@@ -55,7 +59,7 @@ public:
             if (!eat(':')) return false;
             ws();
             if (key == "__metadata__") {
-                if (!skip()) return false;
+                if (!metadata()) return false;
             } else {
                 Entry e;
                 if (!entry(&e)) return false;
@@ -72,6 +76,10 @@ public:
     }
 
 private:
+    // Most containers nested in a header, its top-level object included
+    // (serde_json's default recursion limit, which the safetensors crate's
+    // header parse runs under).
+    static constexpr int kMaxDepth = 128;
     const std::string& s_;
     size_t p_ = 0;
 
@@ -83,24 +91,75 @@ private:
         if (p_ < s_.size() && s_[p_] == c) { ++p_; return true; }
         return false;
     }
+    // Four hex digits of a \u escape at p_.
+    bool hex4(uint32_t* v) {
+        if (s_.size() - p_ < 4) return false;
+        uint32_t x = 0;
+        for (int i = 0; i < 4; ++i) {
+            const char c = s_[p_ + i];
+            const int d = c >= '0' && c <= '9' ? c - '0'
+                        : c >= 'a' && c <= 'f' ? c - 'a' + 10
+                        : c >= 'A' && c <= 'F' ? c - 'A' + 10 : -1;
+            if (d < 0) return false;
+            x = x * 16 + (uint32_t)d;
+        }
+        p_ += 4;
+        *v = x;
+        return true;
+    }
+    static void utf8(uint32_t cp, std::string* out) {
+        if (cp < 0x80) {
+            out->push_back((char)cp);
+        } else if (cp < 0x800) {
+            out->push_back((char)(0xC0 | (cp >> 6)));
+            out->push_back((char)(0x80 | (cp & 0x3F)));
+        } else if (cp < 0x10000) {
+            out->push_back((char)(0xE0 | (cp >> 12)));
+            out->push_back((char)(0x80 | ((cp >> 6) & 0x3F)));
+            out->push_back((char)(0x80 | (cp & 0x3F)));
+        } else {
+            out->push_back((char)(0xF0 | (cp >> 18)));
+            out->push_back((char)(0x80 | ((cp >> 12) & 0x3F)));
+            out->push_back((char)(0x80 | ((cp >> 6) & 0x3F)));
+            out->push_back((char)(0x80 | (cp & 0x3F)));
+        }
+    }
+    // A JSON string, unescaped into *out.  Raw control characters, unknown
+    // escapes, malformed \u escapes and unpaired surrogates are errors (as in
+    // serde_json, which the safetensors crate parses its header with).
     bool str(std::string* out) {
         if (!eat('"')) return false;
         out->clear();
         while (p_ < s_.size() && s_[p_] != '"') {
-            if (s_[p_] == '\\') {
-                ++p_;
-                if (p_ >= s_.size()) return false;
-                const char c = s_[p_];
-                if (c == 'u') {  // keep escaped code points verbatim; tensor names are ASCII
-                    if (p_ + 4 >= s_.size()) return false;
-                    out->append(s_, p_ - 1, 6);
-                    p_ += 5;
-                    continue;
-                }
-                out->push_back(c == 'n' ? '\n' : c == 't' ? '\t' : c);
-                ++p_;
-            } else {
+            const unsigned char b = (unsigned char)s_[p_];
+            if (b < 0x20) return false;
+            if (b != '\\') {
                 out->push_back(s_[p_++]);
+                continue;
+            }
+            if (++p_ >= s_.size()) return false;
+            const char c = s_[p_++];
+            switch (c) {
+            case '"': case '\\': case '/': out->push_back(c); break;
+            case 'b': out->push_back('\b'); break;
+            case 'f': out->push_back('\f'); break;
+            case 'n': out->push_back('\n'); break;
+            case 'r': out->push_back('\r'); break;
+            case 't': out->push_back('\t'); break;
+            case 'u': {
+                uint32_t cp;
+                if (!hex4(&cp)) return false;
+                if (cp >= 0xDC00 && cp < 0xE000) return false;  // lone low surrogate
+                if (cp >= 0xD800 && cp < 0xDC00) {               // high: a low one must follow
+                    uint32_t lo;
+                    if (!eat('\\') || !eat('u') || !hex4(&lo) || lo < 0xDC00 || lo >= 0xE000)
+                        return false;
+                    cp = 0x10000 + ((cp - 0xD800) << 10) + (lo - 0xDC00);
+                }
+                utf8(cp, out);
+                break;
+            }
+            default: return false;
             }
         }
         return eat('"');
@@ -111,6 +170,8 @@ private:
         bool neg = false;
         if (q < s_.size() && s_[q] == '-') { neg = true; ++q; }
         if (q >= s_.size() || s_[q] < '0' || s_[q] > '9') return false;
+        // JSON has no leading zeros
+        if (s_[q] == '0' && q + 1 < s_.size() && s_[q + 1] >= '0' && s_[q + 1] <= '9') return false;
         int64_t x = 0;
         while (q < s_.size() && s_[q] >= '0' && s_[q] <= '9') {
             if (__builtin_mul_overflow(x, (int64_t)10, &x) ||
@@ -155,7 +216,7 @@ private:
                 if (!int_array(&o) || o.size() != 2) return false;
                 e->begin = o[0];
                 e->end = o[1];
-            } else if (!skip()) {
+            } else if (!skip(kMaxDepth - 2)) {  // inside the header and the entry
                 return false;
             }
             ws();
@@ -164,33 +225,100 @@ private:
             return false;
         }
     }
-    bool skip() {  // any JSON value
-        ws();
-        if (p_ >= s_.size()) return false;
-        const char c = s_[p_];
-        if (c == '"') { std::string t; return str(&t); }
-        if (c == '{' || c == '[') {
-            const char close = c == '{' ? '}' : ']';
+    // A JSON number (RFC 8259 grammar: -?(0|[1-9][0-9]*)(.[0-9]+)?([eE][+-]?[0-9]+)?).
+    bool number() {
+        auto digits = [&]() {
+            const size_t q = p_;
+            while (p_ < s_.size() && s_[p_] >= '0' && s_[p_] <= '9') ++p_;
+            return p_ > q;
+        };
+        eat('-');
+        if (eat('0')) {
+        } else if (!digits()) {
+            return false;
+        }
+        if (eat('.') && !digits()) return false;
+        if (p_ < s_.size() && (s_[p_] == 'e' || s_[p_] == 'E')) {
             ++p_;
+            if (!eat('+')) eat('-');
+            if (!digits()) return false;
+        }
+        return true;
+    }
+    bool literal(const char* w) {
+        const size_t n = std::strlen(w);
+        if (s_.compare(p_, n, w) != 0) return false;
+        p_ += n;
+        return true;
+    }
+    // `"__metadata__"`'s value: null or an object of string values (the
+    // safetensors crate reads it as Option<HashMap<String, String>>).
+    bool metadata() {
+        if (literal("null")) return true;
+        if (!eat('{')) return false;
+        ws();
+        if (eat('}')) return true;
+        for (;;) {
+            std::string k, v;
             ws();
-            if (eat(close)) return true;
-            for (;;) {
+            if (!str(&k)) return false;
+            ws();
+            if (!eat(':')) return false;
+            ws();
+            if (!str(&v)) return false;
+            ws();
+            if (eat(',')) continue;
+            return eat('}');
+        }
+    }
+    // Any JSON value, skipped, holding at most max_depth nested containers.
+    // Iterative, so no header can exhaust the stack; anything that is not
+    // JSON fails.
+    bool skip(int max_depth) {
+        char open[kMaxDepth];  // '{' or '[' of each open container
+        if (max_depth > kMaxDepth) max_depth = kMaxDepth;
+        int depth = 0;
+        for (;;) {
+            // one value
+            ws();
+            if (p_ >= s_.size()) return false;
+            const char c = s_[p_];
+            bool opened = false;
+            if (c == '"') {
+                std::string t;
+                if (!str(&t)) return false;
+            } else if (c == '{' || c == '[') {
+                if (depth >= max_depth) return false;
+                open[depth++] = c;
+                ++p_;
                 ws();
-                if (c == '{') {
-                    std::string t;
-                    if (!str(&t)) return false;
-                    ws();
-                    if (!eat(':')) return false;
+                if (eat(c == '{' ? '}' : ']')) {
+                    --depth;  // empty container: a complete value
+                } else {
+                    opened = true;
                 }
-                if (!skip()) return false;
-                ws();
-                if (eat(',')) continue;
-                if (eat(close)) return true;
+            } else if (c == 't' || c == 'f' || c == 'n') {
+                if (!literal(c == 't' ? "true" : c == 'f' ? "false" : "null")) return false;
+            } else if (!number()) {
                 return false;
             }
+            // after a complete value: close containers or go on to the next member
+            for (;;) {
+                if (depth == 0) return true;
+                if (opened) break;  // the first member of a just-opened container
+                ws();
+                if (eat(',')) break;
+                if (!eat(open[depth - 1] == '{' ? '}' : ']')) return false;
+                --depth;
+            }
+            if (open[depth - 1] == '{') {  // a member: "key": value
+                ws();
+                std::string t;
+                if (!str(&t)) return false;
+                ws();
+                if (!eat(':')) return false;
+            }
         }
-        while (p_ < s_.size() && s_[p_] != ',' && s_[p_] != '}' && s_[p_] != ']') ++p_;
-        return true;
     }
 };
 

@@ -23,6 +23,7 @@ constexpr int kMaxDevices = 64;
 
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
+uint64_t g_scratch_gen[kMaxDevices] = {};  // uses of the array per device
 
 // The split-tile arrival counters at the start of the array must start at
 // zero; the GEMMs return them to zero.  A kernel, not a memset: the first
@@ -33,7 +34,7 @@ __global__ void clear_counters_kernel(int32_t* p, int n) {
 
 }  // namespace
 
-int scratch_acquire(int device, hipStream_t s, void** out) {
+int scratch_acquire(int device, hipStream_t s, void** out, uint64_t* gen) {
     if (device < 0 || device >= kMaxDevices)
         return set_error(NOMAS_ERR_INVALID_ARGUMENT, "device %d beyond the %d the scratch array serves",
                          device, kMaxDevices);
@@ -54,7 +55,14 @@ int scratch_acquire(int device, hipStream_t s, void** out) {
         g_scratch_ptr[device] = p;
     }
     *out = g_scratch_ptr[device];
+    *gen = ++g_scratch_gen[device];
     return NOMAS_OK;
+}
+
+uint64_t scratch_generation(int device) {
+    if (device < 0 || device >= kMaxDevices) return 0;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    return g_scratch_gen[device];
 }
 
 }  // namespace nomas

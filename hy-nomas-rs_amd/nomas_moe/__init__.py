@@ -94,7 +94,8 @@ class WeightKey(NomasError):
 
 
 class IoError(NomasError):
-    """Error::Io (error.rs:12-14)."""
+    """A checkpoint that cannot be read or parsed: the reference's
+    Error::Msg("loading {path}: {e}") (weights.rs:112-115), same message form."""
 
 
 _ERRORS = {1: InvalidConfig, 3: WeightKey, 4: IoError}

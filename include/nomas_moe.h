@@ -10,11 +10,12 @@
  *    the message of the last failure on the calling thread is available from
  *    nomas_moe_last_error().  These map onto the reference's error variants
  *    (nomas-core/src/error.rs:7-46): INVALID_CONFIG -> Error::InvalidConfig,
- *    WEIGHT_KEY -> Error::WeightKey, IO -> Error::Io, everything else ->
- *    Error::Candle / Error::Msg.  A checkpoint that cannot be read or parsed
- *    is NOMAS_ERR_IO with the message "loading <path>: <reason>", as
- *    load_dit maps it (weights.rs:112-115).  No entry point lets a C++
- *    exception or an abort escape: failures are always a returned status.
+ *    WEIGHT_KEY -> Error::WeightKey, everything else -> Error::Candle /
+ *    Error::Msg.  A checkpoint that cannot be read or parsed (IO) is the
+ *    reference's Error::Msg("loading <path>: <reason>"): load_dit maps every
+ *    load failure to that message (weights.rs:112-115), and NOMAS_ERR_IO
+ *    carries the same text.  No entry point lets a C++ exception or an abort
+ *    escape: failures are always a returned status.
  *  - Tensors are row-major.  A forward input of any rank >= 2 with last dim D
  *    is passed as `rows` = product of the leading dims, exactly as Lin::fwd
  *    folds leading dims (nomas-core/src/modules/mod.rs:132-134).
@@ -42,7 +43,7 @@ enum nomas_status {
     NOMAS_ERR_INVALID_CONFIG = 1,   /* config.rs:394-399 / shapes unsupported      */
     NOMAS_ERR_INVALID_ARGUMENT = 2, /* null or misaligned pointer, bad row count   */
     NOMAS_ERR_WEIGHT_KEY = 3,       /* weights.rs:117-127 missing / misshaped key  */
-    NOMAS_ERR_IO = 4,               /* checkpoint file could not be read           */
+    NOMAS_ERR_IO = 4,               /* checkpoint unreadable or malformed          */
     NOMAS_ERR_HIP = 5,              /* a HIP runtime call failed                   */
     NOMAS_ERR_OUT_OF_MEMORY = 6,    /* device or host allocation failed            */
     NOMAS_ERR_STATE = 7,            /* e.g. routing read back before any forward   */
@@ -104,15 +105,17 @@ int nomas_moe_forward(nomas_moe_t *h, const void *x, void *y, int64_t rows, void
  * allocate (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  Same arguments and results, but every device buffer of
  * the forward (routing, permuted rows, the SwiGLU intermediate, K-split
- * partials) lives in a static device array of 256 MiB per GPU, held until
+ * partials) lives in a static device array of 512 MiB per GPU, held until
  * the process ends: the call allocates nothing.  `rows` beyond what fits (it
- * depends on dim, hidden and top_k; 3,456 rows at dim 3072, hidden 8192,
- * top-2) is NOMAS_ERR_INVALID_ARGUMENT with the limit in the message.  The
+ * depends on dim, hidden and top_k; 8,128 rows at dim 3072, hidden 8192,
+ * top-2, so one 4,744-row segment of the 8B preset) is
+ * NOMAS_ERR_INVALID_ARGUMENT with the limit in the message.  The
  * first call on a device looks up the array's address and clears its
  * counters with a kernel on `stream`.  All such calls on one GPU share the
  * array: calls that overlap on one GPU (different streams, threads or
- * handles) race, and routing() after such a call reads the array, valid
- * until the next one. */
+ * handles) race, and routing() after such a call reads the array: once
+ * another no-allocation forward has run on the GPU, routing() on the first
+ * handle is NOMAS_ERR_STATE. */
 int nomas_moe_forward_noalloc(nomas_moe_t *h, const void *x, void *y, int64_t rows, void *stream);
 
 /* The FFN half of DiTBlock::forward around the MoE (block.rs:96-101), fused

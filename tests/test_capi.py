@@ -116,7 +116,10 @@ def _load(files, E=2, k=1, D=16, H=8, dtype=0, s=0.0):
     h = C.c_void_p()
     rc = _lib.lib().nomas_moe_from_safetensors(C.byref(c), arr, len(files), b"blocks.0.moe", D, H,
                                                dtype, 0, C.byref(h))
-    return rc, _lib.last_error()
+    msg = _lib.last_error()
+    if h.value:  # loaded (hosts with a GPU)
+        _lib.lib().nomas_moe_destroy(h)
+    return rc, msg
 
 
 def test_checkpoint_missing_expert_keys(tmp_path):
@@ -225,7 +228,10 @@ def _load_ffn(files, D=16, H=8, dtype=0):
     h = C.c_void_p()
     rc = _lib.lib().nomas_ffn_from_safetensors(arr, len(files), b"blocks.0.mlp", D, H, dtype, 0,
                                                C.byref(h))
-    return rc, _lib.last_error()
+    msg = _lib.last_error()
+    if h.value:  # loaded (hosts with a GPU)
+        _lib.lib().nomas_ffn_destroy(h)
+    return rc, msg
 
 
 def test_ffn_checkpoint_missing_keys(tmp_path):
@@ -317,6 +323,133 @@ def test_truncated_and_oversized_headers(tmp_path, loader):
     for p in (short, bigh, liar, junk):
         rc, msg = load([str(p)])
         assert rc == 4 and msg.startswith(f"loading {p}: "), (p.name, rc, msg)
+
+
+def _raw_header_file(path, header: bytes, payload=b""):
+    """Writes a file whose JSON header is the given bytes, verbatim."""
+    with open(path, "wb") as f:
+        f.write(len(header).to_bytes(8, "little"))
+        f.write(header)
+        f.write(payload)
+
+
+_T = b'"t": {"dtype": "F32", "shape": [1], "data_offsets": [0, 4]}'
+
+
+def _nest(opener, depth):
+    if opener == "[":
+        return b"[" * depth + b"]" * depth
+    return b'{"a":' * depth + b"1" + b"}" * depth
+
+
+@pytest.mark.parametrize("loader", ["moe", "ffn"])
+@pytest.mark.parametrize("opener", ["[", "{"])
+@pytest.mark.parametrize("where", ["metadata", "entry_field"])
+def test_deeply_nested_header_is_an_io_error(tmp_path, loader, opener, where):
+    # 100,000 nested containers: the reference's serde_json parse stops at its
+    # recursion limit and load_dit returns Err("loading <path>: ...")
+    # (weights.rs:112-115); the parser here must return, not overflow the stack
+    deep = _nest(opener, 100_000)
+    if where == "metadata":
+        hdr = b'{"__metadata__": ' + deep + b", " + _T + b"}"
+    else:
+        hdr = b'{"t": {"dtype": "F32", "shape": [1], "x": ' + deep + b', "data_offsets": [0, 4]}}'
+    f = str(tmp_path / "deep.safetensors")
+    _raw_header_file(f, hdr, b"\0" * 4)
+    rc, msg = _load([f]) if loader == "moe" else _load_ffn([f])
+    assert rc == 4, (rc, msg)
+    assert msg == f"loading {f}: malformed safetensors header", msg
+
+
+_BAD_JSON = {
+    "bare_word": b'{"t": {"dtype": "F32", "shape": [1], "x": abc, "data_offsets": [0, 4]}}',
+    "bad_literal": b'{"t": {"dtype": "F32", "shape": [1], "x": nul, "data_offsets": [0, 4]}}',
+    "bad_number": b'{"t": {"dtype": "F32", "shape": [1], "x": 1.e5, "data_offsets": [0, 4]}}',
+    "leading_zero": b'{"t": {"dtype": "F32", "shape": [01], "data_offsets": [0, 4]}}',
+    "float_dim": b'{"t": {"dtype": "F32", "shape": [1.0], "data_offsets": [0, 4]}}',
+    "bad_escape": b'{"t": {"dtype": "F32", "shape": [1], "x": "\\q", "data_offsets": [0, 4]}}',
+    "short_unicode": b'{"t": {"dtype": "F32", "shape": [1], "x": "\\u12", "data_offsets": [0, 4]}}',
+    "lone_surrogate": b'{"t": {"dtype": "F32", "shape": [1], "x": "\\udc00", "data_offsets": [0, 4]}}',
+    "control_char": b'{"t": {"dtype": "F32", "shape": [1], "x": "a\x01b", "data_offsets": [0, 4]}}',
+    "metadata_not_strings": b'{"__metadata__": {"a": 1}, ' + _T + b"}",
+    "metadata_array": b'{"__metadata__": [], ' + _T + b"}",
+    "unclosed": b'{"t": {"dtype": "F32", "shape": [1], "x": [1, 2, "data_offsets": [0, 4]}}',
+    "trailing_comma": b'{"t": {"dtype": "F32", "shape": [1], "x": [1, ], "data_offsets": [0, 4]}}',
+    "mismatched_close": b'{"t": {"dtype": "F32", "shape": [1], "x": [1}, "data_offsets": [0, 4]}}',
+    "nest_past_limit": b'{"t": {"dtype": "F32", "shape": [1], "x": ' + _nest("[", 127) +
+                       b', "data_offsets": [0, 4]}}',
+}
+
+
+@pytest.mark.parametrize("case", sorted(_BAD_JSON))
+def test_invalid_json_header_is_an_io_error(tmp_path, case):
+    f = str(tmp_path / f"{case}.safetensors")
+    _raw_header_file(f, _BAD_JSON[case], b"\0" * 4)
+    for load in (_load, _load_ffn):
+        rc, msg = load([f])
+        assert rc == 4, (case, rc, msg)
+        assert msg == f"loading {f}: malformed safetensors header", msg
+
+
+def test_header_json_the_format_allows_is_accepted(tmp_path):
+    # legal JSON the crate accepts: escapes in strings (decoded, so the
+    # unicode-escaped name is the plain key), metadata strings, null
+    # metadata, numbers and nesting below the limit in an ignored field
+    f = str(tmp_path / "moe.safetensors")
+    _checkpoint(f, 2, 16, 8)
+    raw = open(f, "rb").read()
+    n = int.from_bytes(raw[:8], "little")
+    import json
+    hdr = json.loads(raw[8:8 + n])
+    rk = "blocks.0.moe.router.weight"
+    ent = hdr.pop(rk)
+    body = ", ".join(f"{json.dumps(k)}: {json.dumps(v)}" for k, v in hdr.items())
+    router = ('"blocks.0.moe.\\u0072outer.weight": {"dtype": %s, "shape": %s, "x": %s, '
+              '"y": [-1.5e-3, 0, true, false, null, "\\ud83d\\ude00\\n\\/"], "data_offsets": %s}'
+              % (json.dumps(ent["dtype"]), json.dumps(ent["shape"]), _nest("[", 100).decode(),
+                 json.dumps(ent["data_offsets"])))
+    for meta in ('{"format": "pt", "note": "\\"q\\" \\u00e9"}', "null"):
+        text = ('{"__metadata__": %s, %s, %s}' % (meta, router, body)).encode()
+        _raw_header_file(f, text, raw[8 + n:])
+        rc, msg = _load([f])
+        import torch
+        assert rc == (0 if torch.cuda.is_available() else 5), msg
+
+
+def test_header_mutation_fuzz(tmp_path):
+    # seeded mutations of a valid header (byte flips, truncations, inserted
+    # and deleted bytes, deep nests spliced in): every load returns a status
+    # with the reference's message form -- no crash, no hang (the sanitized
+    # suite runs this under ASan/UBSan)
+    f = str(tmp_path / "base.safetensors")
+    _checkpoint(f, 2, 16, 8)
+    raw = open(f, "rb").read()
+    n = int.from_bytes(raw[:8], "little")
+    hdr, payload = raw[8:8 + n], raw[8 + n:]
+    rng = np.random.default_rng(20261202)
+    alphabet = b'{}[]",:0123456789-+.eEtrufalsn \\u\x00\xff'
+    g = str(tmp_path / "mut.safetensors")
+    for it in range(600):
+        h = bytearray(hdr)
+        for _ in range(int(rng.integers(1, 4))):
+            op = int(rng.integers(0, 5))
+            pos = int(rng.integers(0, len(h) + 1))
+            if op == 0 and h:
+                h[min(pos, len(h) - 1)] ^= 1 << int(rng.integers(0, 8))
+            elif op == 1:
+                h = h[:pos]
+            elif op == 2:
+                h[pos:pos] = bytes([alphabet[int(rng.integers(0, len(alphabet)))]])
+            elif op == 3 and h:
+                del h[min(pos, len(h) - 1)]
+            else:
+                h[pos:pos] = _nest("[" if rng.integers(0, 2) else "{", int(rng.integers(100, 5000)))
+        _raw_header_file(g, bytes(h), payload)
+        for load in (_load, _load_ffn):
+            rc, msg = load([g])
+            assert rc in (0, 3, 4, 5), (it, rc, msg)
+            if rc == 4:
+                assert msg.startswith(f"loading {g}: "), (it, msg)
 
 
 def test_well_formed_edge_headers_pass_the_parser(tmp_path):
