@@ -25,6 +25,7 @@ constexpr int kSlabPieces = kSlabBytes / 16;   // 16-byte pieces per row per sla
 constexpr int kProdThreads = kDispThreads / 2; // waves 0-7 load, waves 8-15 store
 constexpr int kDispCUs = 256;                  // MI355X compute units
 constexpr int kDispMaxParts = 8;               // blocks sharing one chunk, at most
+constexpr int kHistInFlight = 16;              // histogram loads in flight per lane
 constexpr int kProdLoads = kRouterRows * kSlabPieces / kProdThreads;  // 4
 static_assert(kProdLoads * kProdThreads == kRouterRows * kSlabPieces, "whole slabs");
 
@@ -115,27 +116,36 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(DispatchArgs a) 
         f3 = fetch(0, 3);
     }
 
-    // 1. histograms: each wave sums every 16th chunk, 16 chunks' counts in
-    // flight per lane (clamped loads, masked values; a chain of single loads
-    // would pay one cache round trip per 16 chunks): one round trip up to 256
-    // chunks
+    // 1. histograms (one per router block of count_rows rows, sub = 64 /
+    // count_rows of them per chunk): each wave sums every 16th histogram, 16
+    // histograms' counts in flight per lane (clamped loads, masked values; a
+    // chain of single loads would pay one round trip per load): one round trip
+    // up to 256 histograms (32 in flight measured 5 us slower, a second round
+    // trip about as much).  The chunk's own counts: threads e < Ec add its sub
+    // histograms.
+    const int sub = kRouterRows / a.count_rows;
+    const int nhist = (int)((a.rows + a.count_rows - 1) / a.count_rows);
+    if (tid < Ec) {
+        int own = 0;
+        for (int h = b * sub; h < min(b * sub + sub, nhist); ++h)
+            own += a.chunk_counts[(int64_t)h * Ec + tid];
+        s_lc[tid] = own;
+    }
     for (int e = lane; e < Ec; e += kWave) {
-        int bef = 0, tot = 0, own = 0;
-        for (int c0 = wave; c0 < nch; c0 += 16 * kDispWaves) {
-            int v[16];
+        int bef = 0, tot = 0;
+        for (int c0 = wave; c0 < nhist; c0 += kHistInFlight * kDispWaves) {
+            int v[kHistInFlight];
 #pragma unroll
-            for (int u = 0; u < 16; ++u)
-                v[u] = a.chunk_counts[(int64_t)min(c0 + u * kDispWaves, nch - 1) * Ec + e];
+            for (int u = 0; u < kHistInFlight; ++u)
+                v[u] = a.chunk_counts[(int64_t)min(c0 + u * kDispWaves, nhist - 1) * Ec + e];
 #pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                const int c = c0 + u * kDispWaves;
-                const int n = c < nch ? v[u] : 0;
+            for (int u = 0; u < kHistInFlight; ++u) {
+                const int h = c0 + u * kDispWaves;
+                const int n = h < nhist ? v[u] : 0;
                 tot += n;
-                bef += c < b ? n : 0;
-                own = c == b ? n : own;
+                bef += h < b * sub ? n : 0;
             }
         }
-        if (wave == b % kDispWaves) s_lc[e] = own;
         s_red[wave * Ec + e] = bef;
         s_red[(kDispWaves + wave) * Ec + e] = tot;
     }
@@ -499,7 +509,8 @@ template <typename T>
 hipError_t launch_dispatch_t(const DispatchArgs& a, hipStream_t s) {
     const int nblk = (int)((a.rows + kRouterRows - 1) / kRouterRows);
     if (nblk == 0) return hipSuccess;
-    if (a.nchunks != nblk || a.E_cols < 1 || a.E_cols > kMaxExperts + 1 || a.k_slots < 1 ||
+    if (a.nchunks != nblk || a.count_rows < kMinRouterBlockRows || a.count_rows > kRouterRows ||
+        kRouterRows % a.count_rows != 0 || a.E_cols < 1 || a.E_cols > kMaxExperts + 1 || a.k_slots < 1 ||
         a.k_slots > a.E_cols || a.BM < 1 || !dispatch_fits(a.E_cols, a.k_slots) ||
         (a.kblocked && (int64_t)a.D * (int64_t)sizeof(T) % kKBlockBytes != 0))
         return hipErrorInvalidValue;

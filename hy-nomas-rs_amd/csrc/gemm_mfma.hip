@@ -78,8 +78,15 @@ template <> struct Mfma<float> {
 
 enum { kGateUp = 0, kDown = 1 };
 
-constexpr int kThreads = 256;
 constexpr int kStages = 4;  // LDS ring depth; the main loop is unrolled over one turn
+// Waves along the token rows of a tile: 2 (4 waves, one per SIMD, 128 x 128
+// outputs each) or 4 (8 waves, two per SIMD, 64 token rows x 128 weight rows
+// each: while one wave of a SIMD waits, the other issues MFMAs).
+#ifndef NOMAS_GEMM_WAVE_ROWS
+#define NOMAS_GEMM_WAVE_ROWS 2
+#endif
+constexpr int kWaveRows = NOMAS_GEMM_WAVE_ROWS;
+static_assert(kWaveRows == 2 || kWaveRows == 4, "2 or 4 waves along the token rows");
 
 // Physical 16-byte chunk of logical chunk c in LDS row r is c ^ swz(r) (4
 // chunks per row).  Any 8 consecutive rows read at one logical chunk then hit
@@ -90,10 +97,11 @@ __device__ __forceinline__ int swz(int r) { return (r >> 1) & 3; }
 // swizzle); with stride 0 the buffer is a plain byte range [0, num_records).
 constexpr int kBufferRsrcWord3 = 0x00020000;
 
-template <typename T, int MODE, int BM, int BN, int BK, int S>
-__global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
+template <typename T, int MODE, int BM, int BN, int BK, int S, int NWM>
+__global__ __launch_bounds__(NWM * 2 * kWave, 1) void gemm_mfma_kernel(GemmArgs a) {
     using V = typename Mfma<T>::V;
-    constexpr int WM = BM / 2, WN = BN / 2;       // wave tile: token rows x weight rows
+    constexpr int kThreads = NWM * 2 * kWave;     // NWM x 2 waves
+    constexpr int WM = BM / NWM, WN = BN / 2;     // wave tile: token rows x weight rows
     constexpr int SM = WM / 16, SN = WN / 16;     // 16x16 MFMA blocks per wave
     constexpr int EPC = 16 / (int)sizeof(T);      // elements per 16-byte chunk
     constexpr int CH = BK / EPC;                  // 16-byte chunks per LDS row
@@ -105,7 +113,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
     constexpr int Q = QW + QX;
     static_assert(BK * (int)sizeof(T) == kKBlockBytes && CH == 4, "64 bytes of k per stage");
     static_assert(S == 4, "ring of 4 stages, the loop unrolled over one turn");
-    static_assert(SN == 8 && SM == 8 && Q == 8, "row schedule: 8 x 8 blocks, 8 loads per step");
+    static_assert(SN == 8 && SM * NWM == 16 && Q * NWM == 16,
+                  "row schedule: 8 rows of SM blocks, Q loads per step");
+    constexpr int RPL = SN / Q;  // rows of the schedule per load (1 or 2)
     static_assert(MODE == kDown || SN % 4 == 0, "gate/up pairs are 2 blocks apart in groups of 4");
     static_assert(BK == kblock_elems<T>(), "operands are K-blocked by the k step");
 
@@ -150,7 +160,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
     const int n0 = nt * BN;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave >> 1, wn = wave & 1;  // wm in [0, NWM)
     const int uwave = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform (SGPR) copy
     const int l16 = lane & 15, lq = lane >> 4;
 
@@ -265,24 +275,24 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < SN / 2; ++i) fa[i] = rdA(0, i);
     __builtin_amdgcn_sched_barrier(0);
-    // A tile of at most WM live token rows leaves the waves of the second
-    // token half (wm = 1) with padding rows only: they skip the MFMAs (their
-    // accumulators keep their start values and the epilogue stores no
-    // padding row) but keep
-    // their share of the loads and every barrier, in the same order as the
-    // loop below.  At the chip's power limit the skipped MFMAs are time saved.
-    const bool pad_half = nrows <= WM && (uwave >> 1) == 1;
-    if (pad_half) {
+    // Waves whose token rows all lie past the tile's live rows (in a tile
+    // of at most WM * wm live rows) hold padding rows only: they skip the
+    // MFMAs (their accumulators keep their start values and the epilogue
+    // stores no padding row) but keep their share of the loads and every
+    // barrier, in the same order as the loop below.  At the chip's power
+    // limit the skipped MFMAs are time saved.
+    const bool pad_wave = (uwave >> 1) * WM >= nrows;
+    if (pad_wave) {
         for (int kt0 = 0; kt0 < KT; kt0 += S) {
 #pragma unroll
             for (int u = 0; u < S; ++u) {
                 const int s = kt0 + u;
 #pragma unroll
-                for (int i = 0; i < SN / 2; ++i) dma(Q / 2 + i, cl(s + 2), (u + 2) % S);
+                for (int q = 0; q < Q / 2; ++q) dma(Q / 2 + q, cl(s + 2), (u + 2) % S);
                 wait_vmcnt<Q>();
                 __builtin_amdgcn_s_barrier();
 #pragma unroll
-                for (int i = SN / 2; i < SN; ++i) dma(i - SN / 2, cl(s + 3), (u + 3) % S);
+                for (int q = 0; q < Q / 2; ++q) dma(q, cl(s + 3), (u + 3) % S);
             }
         }
     } else
@@ -306,10 +316,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
                 for (int j = 0; j < SM; ++j) {
                     acc[i][j] = Mfma<T>::run(fa[i], fb[j], acc[i][j], t);
                     if (t == kSub - 1 && i == SN - 1) fb[j] = rdB((u + 1) % S, j);
-                    if (t == 0 && j == 1) {
+                    if (t == 0 && j == 1 && i % RPL == 0) {
+                        // load q of this half of the stage, every RPL-th row
+                        const int q = (i % (SN / 2)) / RPL;
                         __builtin_amdgcn_sched_barrier(0);
-                        if (i < SN / 2) dma(Q / 2 + i, cl(s + 2), (u + 2) % S);
-                        else dma(i - SN / 2, cl(s + 3), (u + 3) % S);
+                        if (i < SN / 2) dma(Q / 2 + q, cl(s + 2), (u + 2) % S);
+                        else dma(q, cl(s + 3), (u + 3) % S);
                         __builtin_amdgcn_sched_barrier(0);
                     }
                 }
@@ -449,13 +461,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_kernel(GemmArgs a) {
             }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             __builtin_amdgcn_s_barrier();
-            // staging row sr = (wave half h, row w) holds tile row h * WM + rd * kWR + w;
+            // staging row sr = (wave row h, row w) holds tile row h * WM + rd * kWR + w;
             // 8 pieces per thread at a time: their LDS reads all in flight before
             // the first store (one read-to-store latency per 8 pieces, not per piece)
             constexpr int kRowChunks = BN * (int)sizeof(T) / 16;
-            constexpr int kPieces = 2 * kWR * kRowChunks / kThreads;  // per thread per round
+            constexpr int kPieces = NWM * kWR * kRowChunks / kThreads;  // per thread per round
             constexpr int kGrp = 8;
-            static_assert(kPieces * kThreads == 2 * kWR * kRowChunks && kPieces % kGrp == 0,
+            static_assert(kPieces * kThreads == NWM * kWR * kRowChunks && kPieces % kGrp == 0,
                           "whole groups of pieces per thread");
 #pragma unroll
             for (int g0 = 0; g0 < kPieces; g0 += kGrp) {
@@ -499,8 +511,8 @@ hipError_t launch_mfma_t(const GemmArgs& a, hipStream_t s) {
     const int64_t grid = tile_grid(a.max_tiles, a.N / BN) + kSplitUnits;
     if (a.max_tiles <= 0) return hipSuccess;
     if (grid > 0x7fffffff) return hipErrorInvalidValue;
-    launch_kernel((gemm_mfma_kernel<T, MODE, BM, BN, BK, kStages>), dim3((unsigned)grid),
-                  dim3(kThreads), 0, s, a);
+    launch_kernel((gemm_mfma_kernel<T, MODE, BM, BN, BK, kStages, kWaveRows>), dim3((unsigned)grid),
+                  dim3(kWaveRows * 2 * kWave), 0, s, a);
     return hipGetLastError();
 }
 

@@ -77,7 +77,8 @@ struct RouterArgs {
     int32_t* topk_idx;  // rows x k_slots
     float* topk_w;      // rows x k_slots
     float* gap;         // rows
-    int32_t* chunk_counts;  // nchunks x E_cols
+    int32_t* chunk_counts;  // ceil(rows / block_rows) x E_cols: one histogram per router block
+    int block_rows;         // rows per router block: router_block_rows() of this launch
 };
 
 
@@ -96,8 +97,9 @@ struct DispatchArgs {
     int64_t rows;
     int D, E_cols, k_slots;
     const int32_t* topk_idx;
-    const int32_t* chunk_counts;  // nchunks x E_cols, from the router
-    int nchunks;
+    const int32_t* chunk_counts;  // ceil(rows / count_rows) x E_cols, from the router
+    int nchunks;            // 64-row chunks
+    int count_rows;         // rows per histogram (the router's rows per block: 64 or 32)
     int BM;                 // GEMM tile rows
     int max_tiles;
     int32_t* expert_count;  // E_cols
@@ -163,6 +165,13 @@ struct CombineArgs {
 };
 
 size_t router_lds_bytes(int E);
+// Rows per router block (and per histogram it writes) for a launch of
+// `rows` rows: 64, or 32 for small launches that 64-row blocks would leave
+// short of bytes in flight.
+int router_block_rows(DType dt, int64_t rows, int D, int E);
+// Smallest rows per router block: the histogram buffer holds
+// ceil(rows / kMinRouterBlockRows) histograms.
+constexpr int kMinRouterBlockRows = 32;
 // Whether the dispatch kernel's LDS holds E_cols experts and k_slots slots per row.
 bool dispatch_supported(int E_cols, int k_slots);
 

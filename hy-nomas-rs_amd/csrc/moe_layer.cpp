@@ -298,7 +298,6 @@ int MoeLayer::max_tiles(int64_t rows) const {
 
 size_t MoeLayer::layout(int64_t cap, bool block, uint8_t* base, Workspace* w) const {
     const int64_t A = cap * kslots_;
-    const int64_t nch = cap / kRouterRows;
     const size_t es = dtype_size(dt_);
     const int mt = max_tiles(cap);
     size_t off = 0;
@@ -320,7 +319,9 @@ size_t MoeLayer::layout(int64_t cap, bool block, uint8_t* base, Workspace* w) co
     v.w = reinterpret_cast<float*>(take(sizeof(float) * A));
     v.gap = reinterpret_cast<float*>(take(sizeof(float) * cap));
     v.pos = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * A));
-    v.chunk_counts = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * nch * Ecols_));
+    // one histogram per router block, of at least kMinRouterBlockRows rows
+    v.chunk_counts = reinterpret_cast<int32_t*>(
+        take(sizeof(int32_t) * (cap / kMinRouterBlockRows) * Ecols_));
     v.expert_count = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * Ecols_));
     v.expert_off = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * (Ecols_ + 1)));
     v.tiles = reinterpret_cast<TileInfo*>(take(sizeof(TileInfo) * mt));
@@ -516,6 +517,7 @@ int MoeLayer::run_routed(const void* x, void* y, int64_t rows, hipStream_t s,
     ra.topk_w = w.w;
     ra.gap = w.gap;
     ra.chunk_counts = w.chunk_counts;
+    ra.block_rows = router_block_rows(dt_, rows, (int)D_, (int)E_);
     STAGE(launch_router(dt_, ra, s), "router");
     if ((rc = mark(1))) return rc;
 
@@ -532,6 +534,7 @@ int MoeLayer::run_routed(const void* x, void* y, int64_t rows, hipStream_t s,
     da.topk_idx = w.idx;
     da.chunk_counts = w.chunk_counts;
     da.nchunks = nch;
+    da.count_rows = ra.block_rows;
     da.BM = BM_;
     da.max_tiles = mt;
     da.expert_count = w.expert_count;

@@ -271,13 +271,13 @@ __device__ __forceinline__ uint64_t grp_or(uint64_t v) {
     return v;
 }
 
-// Selection for one chunk of kRouterRows rows from its f64 logits (block of
-// NT threads; every thread calls it): softmax, k rounds of argmax (ties to
-// the lowest index), gates p / (sum_sel p + 1e-9), the k-th/best-unselected
-// logit gap, the dense slot, and the chunk's histogram (s_cnt, zeroed by the
+// Selection for one block of RR rows from its f64 logits (block of NT
+// threads; every thread calls it): softmax, k rounds of argmax (ties to the
+// lowest index), gates p / (sum_sel p + 1e-9), the k-th/best-unselected logit
+// gap, the dense slot, and the block's histogram (s_cnt, zeroed by the
 // caller, written to counts_out).  The logits come in NP partial slot sets
-// [NP][kRouterRows][logit_ld(E)] at s_logit, summed in part order.
-template <int NT, int NP = 1>
+// [NP][RR][logit_ld(E)] at s_logit, summed in part order.
+template <int NT, int NP = 1, int RR = kRouterRows>
 __device__ __forceinline__ void select_chunk(const double* s_logit, int* s_cnt, int64_t chunk_row0,
                                              int64_t rows, int E, int k, int k_slots,
                                              float dense_coef, int32_t* __restrict__ topk_idx,
@@ -285,20 +285,20 @@ __device__ __forceinline__ void select_chunk(const double* s_logit, int* s_cnt, 
                                              int32_t* __restrict__ counts_out) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int E_cols = E + (k_slots > k ? 1 : 0);
-    const int part_stride = kRouterRows * logit_ld(E);
+    const int part_stride = RR * logit_ld(E);
     if (E <= kWave) {
         // L lanes per row (a DPP quad, or two in blocks of 512 threads or
         // more): lane sub holds experts sub, sub + L, ... (at most PL) and
         // their logits in registers; max, sums and argmax combine over the
         // group with DPP permutes (xor 1, xor 2 and, for 8 lanes, the half-row
-        // mirror).  The 64 rows take 64 L lanes: one pass of a 256- or
-        // 512-thread block, whole waves idle past them in a larger block.
+        // mirror).  The RR rows take RR L lanes: one pass of the block, whole
+        // waves idle past them.
         // Eight lanes per row halve each lane's dependent chain, and the two
         // waves per SIMD of a 512-thread block hide each other's latencies.
         auto select_rows = [&](auto per_lane, auto lanes) {
             constexpr int PL = decltype(per_lane)::value;
             constexpr int L = decltype(lanes)::value;
-            if (tid >= kRouterRows * L) return;  // whole waves
+            if (tid >= RR * L) return;  // whole waves
             const int lr = tid / L, sub = tid % L;
             const int64_t orow = chunk_row0 + lr;
             const bool ok = orow < rows;  // lanes of missing rows still take part
@@ -372,7 +372,7 @@ __device__ __forceinline__ void select_chunk(const double* s_logit, int* s_cnt, 
                 }
             }
         };
-        if constexpr (NT >= 8 * kRouterRows) {
+        if constexpr (NT >= 8 * RR) {
             using L8 = std::integral_constant<int, 8>;
             if (E <= 16) select_rows(std::integral_constant<int, 2>{}, L8{});
             else select_rows(std::integral_constant<int, 8>{}, L8{});
@@ -385,7 +385,8 @@ __device__ __forceinline__ void select_chunk(const double* s_logit, int* s_cnt, 
         for (int e = tid; e < E_cols; e += NT) counts_out[e] = s_cnt[e];
         return;
     }
-    constexpr int kRowsPerWave = kRouterRows / (NT / kWave);
+    constexpr int kRowsPerWave = RR / (NT / kWave);
+    static_assert(kRowsPerWave * (NT / kWave) == RR, "whole rows per wave");
     const int per_lane = (E + kWave - 1) / kWave;  // experts per lane (<= 4 for E <= 256)
     for (int r = 0; r < kRowsPerWave; ++r) {
         const int lr = wave * kRowsPerWave + r;
@@ -590,9 +591,14 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
 
 // ---- LDS-staged logits: 16-bit inputs, up to 64 experts, D % 128 == 0 -------
 //
-// One block = 8 waves = one chunk of 64 rows.  Waves 0-3 compute the logits
-// and load the router weights; waves 4-7 only load x (they take the same
-// barriers).  All 8 waves run the selection, 8 lanes per row.
+// One block = 8 waves = RR rows (64 or 32; the histogram it writes covers its
+// RR rows).  Waves 0-3 compute the logits and load the router weights;
+// waves 4-7 only load x (they take the same barriers).  The selection runs on
+// 8 lanes per row.
+//  - The x bytes in flight bound the kernel: a block has NST - 1 stages of
+//    its rows in flight, so fewer rows per block with a deeper ring keep more
+//    bytes in flight when the rows alone would leave CUs idle (the plan is
+//    chosen per launch, router_plan).
 //  - x and the router weights stream through an LDS ring of kStages stages,
 //    each 128 elements (256 bytes) of every row of the chunk and of every
 //    expert row.  One direct-to-LDS load fetches 1 KB: four whole 256-byte
@@ -618,8 +624,8 @@ constexpr int kLdsThreads = 2 * kLdsComputeWaves * kWave;  // + 4 waves that loa
 constexpr int kChain = 4;           // k steps accumulated in f32 per f64 add
 constexpr int kLdsMaxExperts = 64;
 
-// ROWB bytes of each row per stage, NST stages in the ring
-template <typename T, int NEG, int ROWB, int NST>
+// ROWB bytes of each row per stage, NST stages in the ring, RR rows per block
+template <typename T, int NEG, int ROWB, int NST, int RR>
 __global__ __launch_bounds__(kLdsThreads) void router_lds_kernel(
     const T* __restrict__ x, const T* __restrict__ wr, int64_t rows, int D, int E, int k,
     int k_slots, float dense_coef, int32_t* __restrict__ topk_idx, float* __restrict__ topk_w,
@@ -631,15 +637,17 @@ __global__ __launch_bounds__(kLdsThreads) void router_lds_kernel(
     constexpr int RPI = 1024 / ROWB;               // rows per 1 KB load
     constexpr int NKP = 4 / NEG;                   // k parts
     constexpr int EP = 16 * NEG;                   // experts, padded to whole groups
-    constexpr int XB = kRouterRows * ROWB;         // x bytes per stage
+    constexpr int NRG = RR / 16;                   // row groups of 16
+    constexpr int XB = RR * ROWB;                  // x bytes per stage
     constexpr int SB = XB + EP * ROWB;             // stage bytes
-    constexpr int QX = kRouterRows / RPI / 4;      // x loads per loading wave per stage
+    constexpr int QX = RR / RPI / 4;               // x loads per loading wave per stage
     constexpr int QW = EP / RPI / 4;               // weight loads per compute wave per stage
     constexpr int KPW = CPR / 4 / NKP;             // this wave's k steps per stage
     constexpr int kRing = NST * SB;
     static_assert(CPR >= 8 && QX >= 1 && QW >= 1 && KPW >= 1, "stage shape");
-    static_assert(NKP * kRouterRows * (16 * NEG + 1) * sizeof(double) <= (size_t)kRing,
+    static_assert(NKP * RR * (16 * NEG + 1) * sizeof(double) <= (size_t)kRing,
                   "the k parts' logit slots fit in the ring");
+    static_assert(RR % 16 == 0 && RR <= kRouterRows && kRouterRows % RR == 0, "row groups of 16");
     __shared__ __attribute__((aligned(16))) unsigned char sRing[kRing];
     __shared__ int s_cnt[kLdsMaxExperts + 1];
     double* const s_logit = reinterpret_cast<double*>(sRing);  // after the k loop
@@ -655,8 +663,8 @@ __global__ __launch_bounds__(kLdsThreads) void router_lds_kernel(
     const int E_cols = E + (k_slots > k ? 1 : 0);
     for (int e = tid; e < E_cols; e += kLdsThreads) s_cnt[e] = 0;
     __syncthreads();  // (before any load is in flight: this barrier may wait for all)
-    const int64_t chunk_row0 = (int64_t)blockIdx.x * kRouterRows;
-    const int nvalid = (int)min<int64_t>(kRouterRows, rows - chunk_row0);
+    const int64_t chunk_row0 = (int64_t)blockIdx.x * RR;
+    const int nvalid = (int)min<int64_t>(RR, rows - chunk_row0);
     const int nstage = D / KS;
 
     // Load q of a stage fills LDS bytes [q * 1 KB, +1 KB): rows RPI q ..
@@ -687,9 +695,12 @@ __global__ __launch_bounds__(kLdsThreads) void router_lds_kernel(
             for (int i = 0; i < QX; ++i)
                 lds_dma16(xc + sc * KS, xoff[i], base + (wave * QX + i) * 1024);
         } else {
+            // weight rows past E (the expert group's padding) are not loaded:
+            // their LDS rows feed only MFMA columns that are never read
 #pragma unroll
             for (int i = 0; i < QW; ++i)
-                lds_dma16(wr + sc * KS, woff[i], base + XB + (wave * QW + i) * 1024);
+                if ((wave * QW + i) * RPI < E)
+                    lds_dma16(wr + sc * KS, woff[i], base + XB + (wave * QW + i) * 1024);
         }
     };
     // operand fragment: row `row` of a region, logical chunk c
@@ -699,16 +710,16 @@ __global__ __launch_bounds__(kLdsThreads) void router_lds_kernel(
     };
 
     typedef float f4 __attribute__((ext_vector_type(4)));
-    f4 acc[4];
-    d4 acc64[4];
+    f4 acc[NRG];
+    d4 acc64[NRG];
 #pragma unroll
-    for (int rg = 0; rg < 4; ++rg) {
+    for (int rg = 0; rg < NRG; ++rg) {
         acc[rg] = f4{0.0f, 0.0f, 0.0f, 0.0f};
         acc64[rg] = d4{0.0, 0.0, 0.0, 0.0};
     }
     auto flush = [&]() {
 #pragma unroll
-        for (int rg = 0; rg < 4; ++rg) {
+        for (int rg = 0; rg < NRG; ++rg) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc64[rg][i] += (double)acc[rg][i];
             acc[rg] = f4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -743,7 +754,7 @@ __global__ __launch_bounds__(kLdsThreads) void router_lds_kernel(
             const int j = kp + jj * NKP;
             const uint4 wf = frag(slot, XB, eg * 16 + r16, 4 * j + g);
 #pragma unroll
-            for (int rg = 0; rg < 4; ++rg) {
+            for (int rg = 0; rg < NRG; ++rg) {
                 const uint4 xf = frag(slot, 0, rg * 16 + r16, 4 * j + g);
                 typename std::conditional<std::is_same<T, __bf16>::value, bf16x8_t, f16x8_t>::type
                     av, bv;
@@ -770,15 +781,16 @@ __global__ __launch_bounds__(kLdsThreads) void router_lds_kernel(
     // k part fills its own slot set, which the selection adds in part order
     const int ex = eg * 16 + r16;
     if (!x_loader && ex < E) {
-        double* part = s_logit + kp * (kRouterRows * logit_ld(E));
+        double* part = s_logit + kp * (RR * logit_ld(E));
 #pragma unroll
-        for (int rg = 0; rg < 4; ++rg)
+        for (int rg = 0; rg < NRG; ++rg)
 #pragma unroll
             for (int i = 0; i < 4; ++i) part[(rg * 16 + 4 * g + i) * logit_ld(E) + ex] = acc64[rg][i];
     }
     __syncthreads();
-    select_chunk<kLdsThreads, NKP>(s_logit, s_cnt, chunk_row0, rows, E, k, k_slots, dense_coef,
-                                   topk_idx, topk_w, gap, chunk_counts + (int64_t)blockIdx.x * E_cols);
+    select_chunk<kLdsThreads, NKP, RR>(s_logit, s_cnt, chunk_row0, rows, E, k, k_slots, dense_coef,
+                                       topk_idx, topk_w, gap,
+                                       chunk_counts + (int64_t)blockIdx.x * E_cols);
 }
 
 template <typename T, int NB>
@@ -795,31 +807,86 @@ hipError_t launch_router_nb(const RouterArgs& a, hipStream_t s, int nblk) {
     return hipGetLastError();
 }
 
-template <typename T, int NEG>
-hipError_t launch_router_lds(const RouterArgs& a, hipStream_t s, int nblk) {
+// The LDS router's shape for a launch: RR rows per block and a ring of NST
+// stages.  What bounds the stream is the x bytes the blocks have in flight
+// together (NST - 1 stages of RR rows each): a block has at most one 64-row
+// chunk's 4-stage ring in flight, and 64-row chunks fill the CUs only from
+// 16,384 rows on.
+//  - Up to 8,192 rows and 32 experts: 32-row blocks with the deepest ring one
+//    block per CU holds (12 stages at 16 experts: 88 KB of x in flight, 5.5
+//    times a 64-row block's).  One 4,680-row segment at 8 experts: 13.3 ->
+//    10.1 us.  Past 256 such blocks the dispatch's bookkeeping needs a second
+//    round trip over the histograms (+5 us at 14,232 rows against 0.6 us
+//    saved here), and with more than 32 experts a stage's weight slices
+//    outweigh a 32-row x slice (64 experts, 16,384 rows: 27.3 -> 29.6 us).
+//  - Otherwise 64-row blocks and a 4-stage ring.
+struct RouterPlan {
+    int rr, nst;
+};
+
+constexpr int kRouterLdsBytes = 152 * 1024;  // ring budget of one block per CU
+constexpr int kRouterSmallRows = 8192;       // 32-row blocks up to here
+
+// Stage bytes of NEG expert groups and RR rows (256-byte row slices).
+constexpr int router_stage_bytes(int rr, int neg) { return (rr + 16 * neg) * 256; }
+// The deepest ring of RR-row blocks one block per CU holds.
+constexpr int router_ring(int rr, int neg) {
+    return std::min(12, kRouterLdsBytes / router_stage_bytes(rr, neg));
+}
+
+RouterPlan router_plan(int64_t rows, int E) {
+    const int neg = E <= 16 ? 1 : (E <= 32 ? 2 : 4);
+    if (rows <= kRouterSmallRows && neg < 4) return {32, router_ring(32, neg)};
+    return {64, std::min(4, router_ring(64, neg))};
+}
+
+template <typename T, int NEG, int RR, int NST>
+hipError_t launch_router_lds_rr(const RouterArgs& a, hipStream_t s) {
     constexpr int ROWB = 256;
-    constexpr int SB = (kRouterRows + 16 * NEG) * ROWB;    // stage bytes
-    constexpr int NST = std::min(4, (152 * 1024) / SB);     // as deep as the LDS allows
-    launch_kernel((router_lds_kernel<T, NEG, ROWB, NST>), dim3(nblk), dim3(kLdsThreads), 0, s,
+    static_assert(NST * router_stage_bytes(RR, NEG) <= kRouterLdsBytes, "the ring fits");
+    const int nblk = (int)((a.rows + RR - 1) / RR);
+    launch_kernel((router_lds_kernel<T, NEG, ROWB, NST, RR>), dim3(nblk), dim3(kLdsThreads), 0, s,
                   (const T*)a.x, (const T*)a.wr, a.rows, a.D, a.E, a.k, a.k_slots,
                   a.dense_coef, a.topk_idx, a.topk_w, a.gap, a.chunk_counts);
     return hipGetLastError();
 }
 
+// The shapes router_plan can ask for at each NEG.
+template <typename T, int NEG>
+hipError_t launch_router_lds(const RouterArgs& a, hipStream_t s, const RouterPlan& p) {
+    constexpr int d64 = std::min(4, router_ring(64, NEG));
+    if (p.rr == 64 && p.nst == d64) return launch_router_lds_rr<T, NEG, 64, d64>(a, s);
+    if constexpr (NEG < 4) {
+        constexpr int d32 = router_ring(32, NEG);
+        if (p.rr == 32 && p.nst == d32) return launch_router_lds_rr<T, NEG, 32, d32>(a, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+// Whether a launch takes the LDS router (16-bit inputs, up to 64 experts,
+// D % 128 == 0).
+bool router_lds_applies(DType dt, int D, int E) {
+    return dt != DType::F32 && E <= kLdsMaxExperts && D % 128 == 0;
+}
+
 template <typename T>
 hipError_t launch_router_t(const RouterArgs& a, hipStream_t s) {
-    const int nblk = (int)((a.rows + kRouterRows - 1) / kRouterRows);
-    if (nblk == 0) return hipSuccess;
+    if (a.rows <= 0) return hipSuccess;
     // f32 inputs (f64 MFMAs, two accumulators per block) take one block per pass
     if constexpr (sizeof(T) == 4) {
-        return launch_router_nb<T, 1>(a, s, nblk);
+        if (a.block_rows != kRouterRows) return hipErrorInvalidValue;
+        return launch_router_nb<T, 1>(a, s, (int)((a.rows + kRouterRows - 1) / kRouterRows));
     } else {
         // LDS-staged logits where they apply (up to 64 experts, D % 128 == 0)
         if (a.E <= kLdsMaxExperts && a.D % 128 == 0) {
-            if (a.E <= 16) return launch_router_lds<T, 1>(a, s, nblk);
-            if (a.E <= 32) return launch_router_lds<T, 2>(a, s, nblk);
-            return launch_router_lds<T, 4>(a, s, nblk);
+            const RouterPlan p = router_plan(a.rows, a.E);
+            if (a.block_rows != p.rr) return hipErrorInvalidValue;
+            if (a.E <= 16) return launch_router_lds<T, 1>(a, s, p);
+            if (a.E <= 32) return launch_router_lds<T, 2>(a, s, p);
+            return launch_router_lds<T, 4>(a, s, p);
         }
+        if (a.block_rows != kRouterRows) return hipErrorInvalidValue;
+        const int nblk = (int)((a.rows + kRouterRows - 1) / kRouterRows);
         if (a.E <= 16) return launch_router_nb<T, 1>(a, s, nblk);
         if (a.E <= 32) return launch_router_nb<T, 2>(a, s, nblk);
         return launch_router_nb<T, 4>(a, s, nblk);
@@ -829,6 +896,10 @@ hipError_t launch_router_t(const RouterArgs& a, hipStream_t s) {
 }  // namespace
 
 size_t router_lds_bytes(int E) { return router_lds(E); }
+
+int router_block_rows(DType dt, int64_t rows, int D, int E) {
+    return router_lds_applies(dt, D, E) ? router_plan(rows, E).rr : kRouterRows;
+}
 
 hipError_t launch_router(DType dt, const RouterArgs& a, hipStream_t s) {
     switch (dt) {

@@ -202,6 +202,24 @@ def test_router_pass_widths(E, k, dtype):
     run_case(330, 256, E, k, 128, dtype, seed=40 + E, router_std=0.2)
 
 
+@pytest.mark.parametrize("rows", [4999, 8192, 8193])
+@pytest.mark.parametrize("E,k", [(16, 2), (32, 4), (64, 8)])
+def test_router_block_plans(rows, E, k):
+    # The 16-bit router's rows per block and ring depth follow the row count
+    # and the experts: up to 8,192 rows and 32 experts, 32-row blocks with a
+    # deep ring (1 or 2 groups of 16 experts), otherwise 64-row blocks (up to
+    # 4 groups).  The dispatch adds the two 32-row histograms of each 64-row
+    # chunk (the last chunk of 4,999 rows has one).  Routing on every row,
+    # outputs on a spread of rows.
+    D, H = 256, 128
+    t, x = small_case(rows, D, E, k, H, 500 + E + rows, router_std=0.2)
+    layer = layer_from_tensors(t, "bf16", D, H, E, k)
+    rt, rx = rounded(t, x, "bf16")
+    p, _ = nm.workloads.oracle_params(rt, E)
+    sel = np.unique(np.r_[np.arange(0, rows, 97), rows - 1])
+    compare(layer, to_device(x, "bf16"), rx, p, k, "bf16", rows=sel)
+
+
 def test_more_than_64_slots_per_row():
     # top-70 of 80: the combine reads slots past 64 from memory, not from lanes
     run_case(100, 256, 80, 70, 128, "bf16", seed=39, router_std=0.2)
