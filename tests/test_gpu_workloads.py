@@ -9,8 +9,11 @@ of its row tiles, including tiles split along K (rows are independent, so
 the oracle evaluates exactly those rows).  Two bars
 against the f64 oracle, and a tight bar against the oracle with the GPU
 path's storage roundings.  Size-independent properties: counts sum to
-rows * k, every row finite, a second forward bitwise identical.
+rows * k, every row finite, a second forward bitwise identical.  The one-segment
+shape also runs as an f16 and an f32 model.
 """
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -25,9 +28,22 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("name", ["seg8b", "cfg8b", "fine64", "skewed16"])
 def test_workload(name):
-    w = wl.WORKLOADS[name]
-    print(f"workload {name}: rows={w.rows} D={w.dim} E={w.experts} k={w.top_k} H={w.hidden}",
-          flush=True)
+    check_workload(wl.WORKLOADS[name])
+
+
+@pytest.mark.parametrize("dt", ["f16", "f32"])
+def test_one_segment_in_other_model_dtypes(dt):
+    # The one-segment 8B shape (4,680 rows, dim 3072, 8 experts, top-2, hidden
+    # 8192) for f16 and f32 models: their own router and MFMA GEMM
+    # instantiations (16x16x32 f16 MFMAs; for f32, f64 router MFMAs and four
+    # 16x16x4 f32 MFMAs per 16-byte fragment) at full size.
+    check_workload(dataclasses.replace(wl.WORKLOADS["seg8b"], dtype=dt))
+
+
+def check_workload(w):
+    name = w.name
+    print(f"workload {name}: rows={w.rows} D={w.dim} E={w.experts} k={w.top_k} H={w.hidden} "
+          f"{w.dtype}", flush=True)
     t = wl.make_params(w)
     x = wl.make_x(w)
     dt = w.dtype
