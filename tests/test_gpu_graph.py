@@ -77,3 +77,41 @@ def test_graph_replays_match_eager(entry, dim, E, k, hidden, dtype, rows):
             run(other, y_other)
         torch.cuda.synchronize()
         assert torch.equal(y_other, eager_other)
+
+
+def test_graph_of_one_8b_segment_without_allocation():
+    # The reference's per-branch call at the 8B preset: 4,744 rows (4,680 video
+    # + 64 text), dim 3072, 8 experts, top-2, hidden 8192, bf16, captured
+    # through the no-allocation entry point (its buffers in the library's
+    # static array), replayed with eager forwards of other row counts between
+    from nomas_moe import workloads as wl
+    w = wl.WORKLOADS["seg8b"]
+    rows = 4744
+    print(f"8B segment graph: rows={rows} D={w.dim} E={w.experts} k={w.top_k} H={w.hidden}",
+          flush=True)
+    layer = nm.MoeLayer.from_source(nm.Weights.from_tensors(wl.make_params(w), w.dtype),
+                                    wl.moe_path(), w.dim, w.hidden, nm.MoeConfig(w.experts, w.top_k))
+    x = _inputs(rows, w.dim, w.dtype, 3)
+    other = _inputs(1000, w.dim, w.dtype, 4)
+    y, y_other = torch.empty_like(x), torch.empty_like(other)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        _noalloc(layer, x, y)  # the array's address is looked up before the capture
+        layer.forward(other, out=y_other)
+    torch.cuda.synchronize()
+    eager, eager_other = y.clone(), y_other.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        _noalloc(layer, x, y)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager), f"replay {rep} differs from the eager forward"
+        with torch.cuda.stream(s):
+            _noalloc(layer, other, y_other)  # the same array, another row count
+        torch.cuda.synchronize()
+        assert torch.equal(y_other, eager_other)
+    print("  3 replays equal the eager forward bit for bit", flush=True)
