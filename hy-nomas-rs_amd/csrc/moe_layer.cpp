@@ -410,7 +410,10 @@ int MoeLayer::forward_impl(const void* x, void* y, int64_t rows, hipStream_t s,
         return forward_dense(x, y, rows, s);
     }
     rc = run_routed(x, y, rows, s, blk, ws_);
-    if (rc != NOMAS_OK) return rc;
+    if (rc != NOMAS_OK) {
+        last_rows_ = -1;  // a failed forward may have overwritten the last one's routing
+        return rc;
+    }
     last_in_scratch_ = false;
     return finish_forward(rows, s, ws_);
 }
@@ -446,7 +449,10 @@ int MoeLayer::forward_noalloc(const void* x, void* y, int64_t rows, hipStream_t 
     layout(cap, false, static_cast<uint8_t*>(base), &w);
     if (done_recorded_ && s != last_stream_) HIP_TRY(hipStreamWaitEvent(s, done_, 0));
     rc = run_routed(x, y, rows, s, nullptr, w);
-    if (rc != NOMAS_OK) return rc;
+    if (rc != NOMAS_OK) {
+        last_rows_ = -1;  // as in forward_impl
+        return rc;
+    }
     last_in_scratch_ = true;
     last_scratch_gen_ = gen;
     return finish_forward(rows, s, w);

@@ -156,7 +156,9 @@ int64_t nomas_moe_n_params(const nomas_moe_t *h);
  * the reference keeps it inside forward, moe.rs:92-95).  idx/w are rows x k
  * with experts in ascending index order, counts has E entries, gap has one
  * entry per row: logit of the k-th selected expert minus the best unselected
- * one (+inf when k == E).  Any pointer may be NULL.  Synchronises. */
+ * one (+inf when k == E).  Any pointer may be NULL.  Synchronises.
+ * NOMAS_ERR_STATE before any forward, and after a forward that failed (its
+ * launches may have overwritten the previous forward's routing). */
 int nomas_moe_routing(nomas_moe_t *h, int32_t *idx, float *w, int32_t *counts, float *gap);
 
 /* Dimensions of a handle: dim, hidden, experts, top_k, dtype (any may be NULL). */
