@@ -7,6 +7,7 @@ graph here is replayed several times, with other forwards of the same layer
 (other inputs, other row counts) and host synchronisations between the
 replays, and every replay must equal the eager forward bit for bit.
 """
+import numpy as np
 import pytest
 import torch
 
@@ -115,3 +116,65 @@ def test_graph_of_one_8b_segment_without_allocation():
         torch.cuda.synchronize()
         assert torch.equal(y_other, eager_other)
     print("  3 replays equal the eager forward bit for bit", flush=True)
+
+
+def _replay_check(run, y, eager, other_run, y_other, eager_other, s, reps=3):
+    g = torch.cuda.CUDAGraph()
+    y.zero_()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=s):
+        run()
+    torch.cuda.synchronize()
+    for rep in range(reps):
+        y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager), f"replay {rep} differs from the eager forward"
+        with torch.cuda.stream(s):
+            other_run()
+        torch.cuda.synchronize()
+        assert torch.equal(y_other, eager_other)
+
+
+@pytest.mark.parametrize("dim,hidden,dtype,rows", [
+    (256, 256, "bf16", 1500),   # MFMA path
+    (192, 96, "f32", 300),      # general path
+])
+def test_graph_of_dense_ffn(dim, hidden, dtype, rows):
+    # the dense feed-forward (mlp.rs:39-48): tile table, K-blocked copy of x
+    # and the two GEMMs, captured once its workspace exists
+    from test_gpu_ffn import PATH as FPATH, ffn_case
+    t, _ = ffn_case(8, dim, hidden, 71)
+    ffn = nm.FeedForward.from_source(nm.Weights.from_tensors(t, dtype), FPATH, dim, hidden)
+    x, other = _inputs(rows, dim, dtype, 5), _inputs(rows // 3 + 1, dim, dtype, 6)
+    y, y_other = torch.empty_like(x), torch.empty_like(other)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        ffn.forward(x, out=y)
+        ffn.forward(other, out=y_other)
+    torch.cuda.synchronize()
+    eager, eager_other = y.clone(), y_other.clone()
+    _replay_check(lambda: ffn.forward(x, out=y), y, eager,
+                  lambda: ffn.forward(other, out=y_other), y_other, eager_other, s)
+
+
+def test_graph_of_block_forward():
+    # the FFN half of a DiT block (block.rs:96-101): norm2 + modulate, the
+    # routed forward and the gated residual in the combine, captured
+    B, S, D, E, k, H = 2, 300, 256, 8, 2, 384
+    layer = _layer(D, E, k, H, "bf16", 77)
+    rng = np.random.default_rng(9)
+    x = to_device((rng.standard_normal((B * S, D)) * 1.7).astype(np.float32), "bf16").reshape(B, S, D)
+    sh, sc, g, nw = (torch.from_numpy((rng.standard_normal(n) * 0.5).astype(np.float32)).cuda()
+                     for n in ((B, D), (B, D), (B, D), (D,)))
+    other = _inputs(500, D, "bf16", 7)
+    y, y_other = torch.empty_like(x), torch.empty_like(other)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        layer.forward_block(x, sh, sc, g, nw, out=y)
+        layer.forward(other, out=y_other)
+    torch.cuda.synchronize()
+    eager, eager_other = y.clone(), y_other.clone()
+    _replay_check(lambda: layer.forward_block(x, sh, sc, g, nw, out=y), y, eager,
+                  lambda: layer.forward(other, out=y_other), y_other, eager_other, s)
