@@ -155,3 +155,31 @@ def test_stage_profiling():
     assert set(st) == set(nm.FeedForward.STAGES)
     assert st["gemm_gate_up"] > 0 and st["gemm_down"] > 0
     assert st["router"] == 0 and st["combine"] == 0  # no such stages: no kernel, zero time
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_preset_8b_dense_ffn_full_size(dtype):
+    # What the shipped 8B preset runs (moe: None, config.rs:297-330): the
+    # dense SwiGLU FFN at dim 3072, hidden 3072 * 4.0 = 12288 (block.rs:38),
+    # on one 4,744-row segment (4,680 video + 64 text rows), Weights::Random
+    # (xavier weights, zero biases: mod.rs:80-95).  Rows at six offsets of
+    # every 256-row GEMM tile (both wave halves, the last tile's tail) are
+    # checked against the oracle in f64.
+    D, H, rows, seed = 3072, 12288, 4744, 0x5EED0000
+    print(f"8B dense FFN rows={rows} D={D} H={H} {dtype}", flush=True)
+    ffn = nm.FeedForward.from_source(nm.Weights.random(seed, dtype), PATH, D, H)
+    assert ffn.uses_mfma
+    x = nm.randn_affine(nm.path_seed(seed, "x"), rows * D).reshape(rows, D)
+    y = ffn.forward(to_device(x, dtype))
+    torch.cuda.synchronize()
+    got = y.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    sel = np.unique(np.minimum(
+        (np.arange(0, rows, 256)[:, None] + np.array([0, 53, 127, 128, 199, 255])[None, :]).ravel(),
+        rows - 1))
+    f = {k: nm.widen(nm.to_model_dtype(O.xavier(o, i, O.path_seed(seed, f"{PATH}.{n}")), dtype), dtype)
+         for k, n, o, i in (("wg", "gate", H, D), ("wu", "up", H, D), ("wd", "down", D, H))}
+    xr = nm.widen(nm.to_model_dtype(x[sel], dtype), dtype)
+    err = rel_err(got[sel], O.ffn(xr, f))
+    print(f"  rel err {err:.3e} on {sel.size} rows", flush=True)
+    assert err <= TOL[dtype], f"relative error {err:.3e} above {TOL[dtype]}"
