@@ -9,7 +9,8 @@ scan, dispatch, gate/up GEMM, down GEMM, combine) with x already resident in
 HBM.  Prints one JSON line.
 
   python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
-                  [--ffn | --block | --vendor-gemm | --hbm-yardstick | --host-tensors]
+                  [--ffn [--ffn-hidden H] | --block | --vendor-gemm | --hbm-yardstick |
+                   --host-tensors]
 """
 from __future__ import annotations
 
@@ -389,6 +390,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="cfg8b")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--ffn-hidden", type=int, default=0,
+                    help="with --ffn: the FFN's hidden size instead of the workload's (12288 is "
+                         "the 8B preset's dense FFN, dim 3072 x mlp_ratio 4.0)")
     ap.add_argument("--ffn", action="store_true",
                     help="time the dense SwiGLU feed-forward (one expert, no routing) at the "
                          "workload's dim, hidden and rows instead of the MoE block")
@@ -421,6 +425,9 @@ def main() -> int:
 
     w = wl.WORKLOADS[args.workload]
     if args.ffn:
+        if args.ffn_hidden:
+            import dataclasses
+            w = dataclasses.replace(w, hidden=args.ffn_hidden)
         return bench_ffn(args, w)
     if args.block:
         return bench_block(args, w)
