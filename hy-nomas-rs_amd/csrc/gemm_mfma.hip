@@ -199,15 +199,32 @@ __global__ __launch_bounds__(NWM * 2 * kWave, 1) void gemm_mfma_kernel(GemmArgs 
     // load q (0..Q-1) of step kt into ring slot `slot`: q < QW are weight
     // rows, the rest token rows
     const int xbytes = nrows * BK * (int)sizeof(T);  // one K-block's live token rows
+    // The loads of one operand and step go out as a group (q = 0.. or
+    // QW.., in order): load q of a wave fills the 1 KB LDS block after load
+    // q - 1's and reads the 1 KB after its global run (woff[q] = woff[0] +
+    // 1 KB q, likewise xoff), so the group shares one M0 write and each load
+    // carries its 1 KB step in the immediate offset.  16-bit types only: in
+    // the f32 down kernel (four times the MFMAs per load) the register
+    // allocator then spills 416 bytes per lane instead of 56.
+    static_assert(RPI * BK * (int)sizeof(T) == 1024 && QW <= 4 && QX <= 4, "1 KB per load, 4 at most");
     auto dma = [&](int q, int kt, int slot) {
-        if (q < QW)
-            lds_dma16(Wt + kt * wstep, woff[q],
-                      lds_addr(stW(slot)) + (uwave * QW + q) * RPI * BK * (int)sizeof(T));
-        else
-            lds_dma16_buf(__builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(Xt + kt * xstep), 0, xbytes,
-                                                            kBufferRsrcWord3),
-                          xoff[q - QW],
-                          lds_addr(stX(slot)) + (uwave * QX + q - QW) * RPI * BK * (int)sizeof(T));
+        if constexpr (sizeof(T) == 4) {
+            if (q < QW)
+                lds_dma16(Wt + kt * wstep, woff[q], lds_addr(stW(slot)) + (uwave * QW + q) * 1024);
+            else
+                lds_dma16_buf(__builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(Xt + kt * xstep), 0, xbytes,
+                                                                kBufferRsrcWord3),
+                              xoff[q - QW], lds_addr(stX(slot)) + (uwave * QX + q - QW) * 1024);
+        } else if (q < QW) {
+            if (q == 0) set_lds_m0(lds_addr(stW(slot)) + uwave * QW * 1024);
+            lds_dma16_q(q, Wt + kt * wstep, woff[0]);
+        } else {
+            if (q == QW) set_lds_m0(lds_addr(stX(slot)) + uwave * QX * 1024);
+            lds_dma16_buf_q(q - QW,
+                            __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(Xt + kt * xstep), 0, xbytes,
+                                                              kBufferRsrcWord3),
+                            xoff[0]);
+        }
     };
     // operand fragments: lane (l16, lq) holds row l16 of a 16-row block, k chunk lq
     auto rdA = [&](int slot, int i) -> V {

@@ -36,7 +36,42 @@ __device__ __forceinline__ void lds_dma16_buf(__amdgpu_buffer_rsrc_t rsrc, uint3
                  : "v"(voff), "s"(rsrc), "s"(lds_base)
                  : "memory", "m0");
 }
+// Groups of loads into consecutive 1 KB LDS blocks: M0 is written once per
+// group (set_lds_m0) and load q of the group carries q * 1024 in its
+// immediate offset, which the hardware adds to both the global (or buffer)
+// address and the LDS address.  One M0 write and wait state per group
+// instead of per load.
+__device__ __forceinline__ void set_lds_m0(uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0" : : "s"(lds_base) : "memory", "m0");
+}
+template <int OFF>
+__device__ __forceinline__ void lds_dma16_at(const void* sbase, uint32_t voff) {
+    asm volatile("global_load_lds_dwordx4 %0, %1 offset:%2" : : "v"(voff), "s"(sbase), "n"(OFF)
+                 : "memory");
+}
+template <int OFF>
+__device__ __forceinline__ void lds_dma16_buf_at(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff) {
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen offset:%2 lds" : : "v"(voff), "s"(rsrc), "n"(OFF)
+                 : "memory");
+}
 #pragma clang diagnostic pop
+// Load q (0-3, a constant after unrolling) of a group.
+__device__ __forceinline__ void lds_dma16_q(int q, const void* sbase, uint32_t voff) {
+    switch (q) {
+        case 0: lds_dma16_at<0>(sbase, voff); break;
+        case 1: lds_dma16_at<1024>(sbase, voff); break;
+        case 2: lds_dma16_at<2048>(sbase, voff); break;
+        default: lds_dma16_at<3072>(sbase, voff); break;
+    }
+}
+__device__ __forceinline__ void lds_dma16_buf_q(int q, __amdgpu_buffer_rsrc_t rsrc, uint32_t voff) {
+    switch (q) {
+        case 0: lds_dma16_buf_at<0>(rsrc, voff); break;
+        case 1: lds_dma16_buf_at<1024>(rsrc, voff); break;
+        case 2: lds_dma16_buf_at<2048>(rsrc, voff); break;
+        default: lds_dma16_buf_at<3072>(rsrc, voff); break;
+    }
+}
 
 // The LDS byte address of a __shared__ object (for M0).
 template <typename P>
